@@ -1,0 +1,15 @@
+"""MI355X (gfx950) backend for Affon's affine group-wise weight-quantized linear path.
+
+The product is the native library ``libaffon_rocm.so`` (C ABI in
+``include/affon_rocm.h``); this package is the host-side mirror of the
+reference's ``affon:ops`` / Session surface over that ABI.
+"""
+from .core import Executable, FormalTensor, Program, Session, Tensor, TensorSpec, program
+from .ops import (dequantize, quantize, quantized_matmul, quantized_matmul_into, selected_implementation, slice,
+                  transpose)
+
+__all__ = [
+    "Executable", "FormalTensor", "Program", "Session", "Tensor", "TensorSpec", "program",
+    "dequantize", "quantize", "quantized_matmul", "quantized_matmul_into", "selected_implementation", "slice",
+    "transpose",
+]

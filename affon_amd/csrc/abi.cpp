@@ -1,0 +1,513 @@
+// C ABI of the rocm quantized-linear backend: sessions, device memory,
+// validation, implementation selection and the host-pointer drop-in.
+//
+// Validation mirrors the reference exactly:
+//   src/js/compute/program.ts:481-494      (operand dtypes, bits, group, shapes)
+//   src/support/compute_core_cyna.zig:1000-1022 (overflow-checked counts)
+// and rejects before any device work, leaving the output untouched.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <mutex>
+#include <string>
+
+#include "affon_rocm.h"
+#include "internal.h"
+
+struct affon_rocm_session {
+  int device = 0;
+  hipStream_t stream = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* format, ...) {
+  char buffer[512];
+  va_list args;
+  va_start(args, format);
+  std::vsnprintf(buffer, sizeof(buffer), format, args);
+  va_end(args);
+  g_last_error = buffer;
+  return status;
+}
+
+int hip_fail(hipError_t error, const char* what) {
+  return fail(AFFON_ROCM_HIP_ERROR, "%s: %s", what, hipGetErrorString(error));
+}
+
+void clear_error() { g_last_error.clear(); }
+
+bool mul_ok(uint64_t a, uint64_t b, uint64_t* out) {
+  if (a != 0 && b > std::numeric_limits<uint64_t>::max() / a) return false;
+  *out = a * b;
+  return true;
+}
+
+bool add_ok(uint64_t a, uint64_t b, uint64_t* out) {
+  if (b > std::numeric_limits<uint64_t>::max() - a) return false;
+  *out = a + b;
+  return true;
+}
+
+int element_size(int dtype) {
+  switch (dtype) {
+    case AFFON_ROCM_F32: return 4;
+    case AFFON_ROCM_BF16: return 2;
+    case AFFON_ROCM_U32: return 4;
+    default: return 0;
+  }
+}
+
+bool is_float_dtype(int dtype) { return dtype == AFFON_ROCM_F32 || dtype == AFFON_ROCM_BF16; }
+
+// Checks that every element a view names lies inside its allocation.
+int check_view(const affon_rocm_view& v, const char* name) {
+  const int esize = element_size(v.dtype);
+  if (v.data == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s has no data", name);
+  if (v.shape[0] <= 0 || v.shape[1] <= 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s has an empty dimension", name);
+  if (v.stride[0] < 0 || v.stride[1] < 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s has a negative stride", name);
+  if (v.byte_offset % static_cast<size_t>(esize) != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s byte offset is not element aligned", name);
+  uint64_t last0 = 0, last1 = 0, last = 0, bytes = 0, end = 0;
+  if (!mul_ok(static_cast<uint64_t>(v.shape[0] - 1), static_cast<uint64_t>(v.stride[0]), &last0) ||
+      !mul_ok(static_cast<uint64_t>(v.shape[1] - 1), static_cast<uint64_t>(v.stride[1]), &last1) ||
+      !add_ok(last0, last1, &last) || !add_ok(last, 1, &last) ||
+      !mul_ok(last, static_cast<uint64_t>(esize), &bytes) ||
+      !add_ok(bytes, static_cast<uint64_t>(v.byte_offset), &end))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s extent overflows", name);
+  if (end > v.buffer_bytes)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s view exceeds its buffer (%llu > %llu bytes)", name,
+                static_cast<unsigned long long>(end), static_cast<unsigned long long>(v.buffer_bytes));
+  return AFFON_ROCM_OK;
+}
+
+// program.ts:483-493 and compute_core_cyna.zig:1012-1022.
+int validate(const affon_rocm_qmm_desc* d, affon::QmmProblem* p) {
+  if (d == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul descriptor is null");
+  if (d->bits != 2 && d->bits != 4 && d->bits != 8)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul bits must be 2, 4, or 8");
+  if (d->group_size == 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul group_size must be a positive integer");
+  if (!is_float_dtype(d->input.dtype) || d->packed.dtype != AFFON_ROCM_U32 || !is_float_dtype(d->scales.dtype) ||
+      d->biases.dtype != d->scales.dtype)
+    return fail(AFFON_ROCM_INVALID_SHAPE,
+                "quantized_matmul requires f32/bf16 input, u32 weights, and matching f32/bf16 scales and biases");
+  const int64_t M = d->input.shape[0], K = d->input.shape[1], N = d->packed.shape[0];
+  const int64_t per_word = 32 / static_cast<int64_t>(d->bits);
+  const int64_t g = static_cast<int64_t>(d->group_size);
+  if (M <= 0 || K <= 0 || N <= 0 || K % per_word != 0 || K % g != 0 || d->packed.shape[1] != K / per_word ||
+      d->scales.shape[0] != N || d->scales.shape[1] != K / g || d->biases.shape[0] != N ||
+      d->biases.shape[1] != K / g)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul packed or group dimensions do not match input features");
+  int status;
+  if ((status = check_view(d->input, "input")) != AFFON_ROCM_OK) return status;
+  if ((status = check_view(d->packed, "packed")) != AFFON_ROCM_OK) return status;
+  if ((status = check_view(d->scales, "scales")) != AFFON_ROCM_OK) return status;
+  if ((status = check_view(d->biases, "biases")) != AFFON_ROCM_OK) return status;
+  uint64_t out_count = 0, out_bytes = 0;
+  if (!mul_ok(static_cast<uint64_t>(M), static_cast<uint64_t>(N), &out_count) || !mul_ok(out_count, 4, &out_bytes))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul output size overflows");
+  if (d->output == nullptr || d->output_bytes < out_bytes)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul output buffer is smaller than [M,N] f32");
+  if (d->implementation < AFFON_ROCM_IMPL_AUTO || d->implementation > AFFON_ROCM_IMPL_MFMA)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul unknown implementation %d", d->implementation);
+  if (d->numerical_policy < AFFON_ROCM_BACKEND_EQUIVALENT || d->numerical_policy > AFFON_ROCM_APPROXIMATE)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul unknown numerical policy %d", d->numerical_policy);
+
+  p->M = M;
+  p->N = N;
+  p->K = K;
+  p->bits = static_cast<int>(d->bits);
+  p->group = g;
+  p->x = static_cast<const uint8_t*>(d->input.data) + d->input.byte_offset;
+  p->xs0 = d->input.stride[0];
+  p->xs1 = d->input.stride[1];
+  p->x_dtype = d->input.dtype;
+  p->w = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(d->packed.data) + d->packed.byte_offset);
+  p->ws0 = d->packed.stride[0];
+  p->ws1 = d->packed.stride[1];
+  p->s = static_cast<const uint8_t*>(d->scales.data) + d->scales.byte_offset;
+  p->ss0 = d->scales.stride[0];
+  p->ss1 = d->scales.stride[1];
+  p->b = static_cast<const uint8_t*>(d->biases.data) + d->biases.byte_offset;
+  p->bs0 = d->biases.stride[0];
+  p->bs1 = d->biases.stride[1];
+  p->p_dtype = d->scales.dtype;
+  p->out = d->output;
+  return AFFON_ROCM_OK;
+}
+
+// Registered candidates, in the order AUTO prefers them.
+struct Candidate {
+  int impl;
+  const char* id;
+  int version;
+  // 0 exact (bit-identical to the ordered CPU loop), 1 reassociated,
+  // 2 approximate (rounds decoded weights to bf16).
+  int numerical_class;
+  bool (*supports)(const affon::QmmProblem&);
+  hipError_t (*launch)(const affon::QmmProblem&, hipStream_t);
+};
+
+const Candidate kCandidates[] = {
+    {AFFON_ROCM_IMPL_MFMA, "rocm_quantized_matmul.mfma", 1, 2, affon::mfma_supports, affon::mfma_launch},
+    {AFFON_ROCM_IMPL_GEMV_MFMA, "rocm_quantized_matmul.gemv_mfma", 1, 1, affon::gemv_mfma_supports,
+     affon::gemv_mfma_launch},
+    {AFFON_ROCM_IMPL_GEMV, "rocm_quantized_matmul.gemv", 1, 1, affon::gemv_supports, affon::gemv_launch},
+    {AFFON_ROCM_IMPL_GENERIC, "rocm_quantized_matmul.generic", 1, 0, affon::generic_supports,
+     affon::generic_launch},
+};
+
+bool policy_accepts(int policy, int numerical_class) {
+  switch (policy) {
+    case AFFON_ROCM_EXACT_ONLY: return numerical_class == 0;
+    case AFFON_ROCM_BACKEND_EQUIVALENT: return numerical_class <= 1;
+    default: return true;
+  }
+}
+
+// Shape rule for AUTO among candidates that pass their guards: the prefill
+// GEMM for M >= 64, the MFMA decode kernel for 4 <= M <= 16 with bf16 input,
+// the VALU decode kernel otherwise, the generic kernel last.
+bool auto_prefers(const Candidate& c, const affon::QmmProblem& p) {
+  switch (c.impl) {
+    case AFFON_ROCM_IMPL_MFMA: return p.M >= 64;
+    case AFFON_ROCM_IMPL_GEMV_MFMA: return p.M >= 4 && p.M <= 16;
+    default: return true;
+  }
+}
+
+int select(const affon_rocm_qmm_desc* d, const affon::QmmProblem& p, const Candidate** out) {
+  for (const Candidate& c : kCandidates) {
+    if (d->implementation != AFFON_ROCM_IMPL_AUTO && d->implementation != c.impl) continue;
+    if (!policy_accepts(d->numerical_policy, c.numerical_class)) {
+      if (d->implementation == c.impl)
+        return fail(AFFON_ROCM_UNSUPPORTED, "%s is not allowed under the requested numerical policy", c.id);
+      continue;
+    }
+    if (!c.supports(p)) {
+      if (d->implementation == c.impl)
+        return fail(AFFON_ROCM_UNSUPPORTED, "%s cannot run this shape or layout", c.id);
+      continue;
+    }
+    if (d->implementation == AFFON_ROCM_IMPL_AUTO && !auto_prefers(c, p)) continue;
+    *out = &c;
+    return AFFON_ROCM_OK;
+  }
+  return fail(AFFON_ROCM_UNSUPPORTED, "no quantized_matmul implementation accepts this problem");
+}
+
+int check_session(affon_rocm_session* s) {
+  if (s == nullptr || s->stream == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "session is not open");
+  hipError_t e = hipSetDevice(s->device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  return AFFON_ROCM_OK;
+}
+
+bool is_gfx950(int device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int affon_rocm_device_count(int* count) {
+  clear_error();
+  if (count == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "count is null");
+  *count = 0;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e == hipErrorNoDevice) return AFFON_ROCM_OK;
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  for (int i = 0; i < n; ++i) *count += is_gfx950(i) ? 1 : 0;
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_session_create(int device, affon_rocm_session** out) {
+  clear_error();
+  if (out == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "session output is null");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || device < 0 || device >= n)
+    return fail(AFFON_ROCM_UNSUPPORTED, "rocm backend unavailable: no HIP device %d", device);
+  if (!is_gfx950(device)) return fail(AFFON_ROCM_UNSUPPORTED, "rocm backend unavailable: device %d is not gfx950", device);
+  if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+  hipStream_t stream = nullptr;
+  if ((e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)) != hipSuccess) return hip_fail(e, "hipStreamCreate");
+  auto* session = new affon_rocm_session;
+  session->device = device;
+  session->stream = stream;
+  *out = session;
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_session_destroy(affon_rocm_session* session) {
+  clear_error();
+  if (session == nullptr) return AFFON_ROCM_OK;
+  int status = AFFON_ROCM_OK;
+  if (hipSetDevice(session->device) == hipSuccess && session->stream != nullptr) {
+    hipError_t e = hipStreamSynchronize(session->stream);
+    if (e != hipSuccess) status = hip_fail(e, "hipStreamSynchronize");
+    e = hipStreamDestroy(session->stream);
+    if (e != hipSuccess && status == AFFON_ROCM_OK) status = hip_fail(e, "hipStreamDestroy");
+  }
+  delete session;
+  return status;
+}
+
+void* affon_rocm_session_stream(affon_rocm_session* session) {
+  return session == nullptr ? nullptr : static_cast<void*>(session->stream);
+}
+
+int affon_rocm_alloc(affon_rocm_session* session, size_t bytes, void** out) {
+  clear_error();
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  if (out == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "allocation output is null");
+  *out = nullptr;
+  hipError_t e = hipMalloc(out, bytes == 0 ? 1 : bytes);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_free(affon_rocm_session* session, void* ptr) {
+  clear_error();
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  if (ptr == nullptr) return AFFON_ROCM_OK;
+  hipError_t e = hipStreamSynchronize(session->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  e = hipFree(ptr);
+  if (e != hipSuccess) return hip_fail(e, "hipFree");
+  return AFFON_ROCM_OK;
+}
+
+static int copy(affon_rocm_session* session, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+  clear_error();
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  if (bytes == 0) return AFFON_ROCM_OK;
+  if (dst == nullptr || src == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "copy with a null pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
+  e = hipStreamSynchronize(session->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_memcpy_h2d(affon_rocm_session* session, void* dst, const void* src, size_t bytes) {
+  return copy(session, dst, src, bytes, hipMemcpyHostToDevice);
+}
+
+int affon_rocm_memcpy_d2h(affon_rocm_session* session, void* dst, const void* src, size_t bytes) {
+  return copy(session, dst, src, bytes, hipMemcpyDeviceToHost);
+}
+
+int affon_rocm_memcpy_d2d(affon_rocm_session* session, void* dst, const void* src, size_t bytes) {
+  return copy(session, dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+int affon_rocm_synchronize(affon_rocm_session* session) {
+  clear_error();
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  hipError_t e = hipStreamSynchronize(session->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  return AFFON_ROCM_OK;
+}
+
+const char* affon_rocm_last_error(void) { return g_last_error.c_str(); }
+
+int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qmm_desc* desc) {
+  clear_error();
+  affon::QmmProblem p;
+  int status = validate(desc, &p);
+  if (status != AFFON_ROCM_OK) return status;
+  const Candidate* c = nullptr;
+  if ((status = select(desc, p, &c)) != AFFON_ROCM_OK) return status;
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  hipError_t e = c->launch(p, session->stream);
+  if (e != hipSuccess) return hip_fail(e, c->id);
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_quantized_matmul_select(const affon_rocm_qmm_desc* desc, char* id, size_t cap) {
+  clear_error();
+  affon::QmmProblem p;
+  int status = validate(desc, &p);
+  if (status != AFFON_ROCM_OK) return status;
+  const Candidate* c = nullptr;
+  if ((status = select(desc, p, &c)) != AFFON_ROCM_OK) return status;
+  if (id != nullptr && cap > 0) {
+    std::strncpy(id, c->id, cap - 1);
+    id[cap - 1] = '\0';
+  }
+  return AFFON_ROCM_OK;
+}
+
+const char* affon_rocm_quantized_matmul_capabilities(void) {
+  static const char* kJson =
+      "["
+      "{\"id\":\"rocm_quantized_matmul.mfma\",\"version\":1,\"numerical_class\":\"approximate\","
+      "\"guard\":\"gfx950; bf16 input; group_size % 32 == 0; K % 64 == 0; unit inner strides; M >= 64 when auto\","
+      "\"note\":\"decoded weights rounded to bf16 in LDS, bf16 MFMA, f32 accumulation\"},"
+      "{\"id\":\"rocm_quantized_matmul.gemv_mfma\",\"version\":1,\"numerical_class\":\"reassociated\","
+      "\"guard\":\"gfx950; bf16 input; M <= 16; group_size % 32 == 0; unit inner strides\","
+      "\"note\":\"integer codes exact in bf16, per-group scale and bias applied in f32\"},"
+      "{\"id\":\"rocm_quantized_matmul.gemv\",\"version\":1,\"numerical_class\":\"reassociated\","
+      "\"guard\":\"gfx950; group_size % (32/bits) == 0; unit inner strides; aligned rows\","
+      "\"note\":\"VALU decode, f32 accumulation, per-group scale and bias applied in f32\"},"
+      "{\"id\":\"rocm_quantized_matmul.generic\",\"version\":1,\"numerical_class\":\"exact\","
+      "\"guard\":\"gfx950; any strides, byte offsets and group sizes\","
+      "\"note\":\"ordered f32 loop per output, separately rounded products and sums\"}"
+      "]";
+  return kJson;
+}
+
+int affon_rocm_quantize(affon_rocm_session* session, const void* weights, int32_t weight_dtype, int64_t rows,
+                        int64_t columns, uint32_t bits, uint32_t group_size, uint32_t* packed, void* scales,
+                        void* biases, int32_t param_dtype) {
+  clear_error();
+  if (bits != 2 && bits != 4 && bits != 8) return fail(AFFON_ROCM_INVALID_SHAPE, "quantize bits must be 2, 4, or 8");
+  if (group_size == 0) return fail(AFFON_ROCM_INVALID_SHAPE, "quantize group_size must be a positive integer");
+  if (!is_float_dtype(weight_dtype) || !is_float_dtype(param_dtype))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantize requires f32/bf16 weights and f32/bf16 parameters");
+  const int64_t per_word = 32 / static_cast<int64_t>(bits);
+  if (rows <= 0 || columns <= 0 || columns % per_word != 0 || columns % static_cast<int64_t>(group_size) != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantize columns must divide into complete words and groups");
+  uint64_t count = 0;
+  if (!mul_ok(static_cast<uint64_t>(rows), static_cast<uint64_t>(columns), &count) || count > (uint64_t(1) << 60))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantize size overflows");
+  if (weights == nullptr || packed == nullptr || scales == nullptr || biases == nullptr)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantize buffer is null");
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::quantize_launch(weights, weight_dtype, rows, columns, static_cast<int>(bits), group_size,
+                                        packed, scales, biases, param_dtype, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "quantize");
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_dequantize(affon_rocm_session* session, const uint32_t* packed, const void* scales, const void* biases,
+                          int32_t param_dtype, int64_t rows, int64_t columns, uint32_t bits, uint32_t group_size,
+                          void* out, int32_t out_dtype) {
+  clear_error();
+  if (bits != 2 && bits != 4 && bits != 8)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "dequantize bits must be 2, 4, or 8");
+  if (group_size == 0) return fail(AFFON_ROCM_INVALID_SHAPE, "dequantize group_size must be a positive integer");
+  if (!is_float_dtype(param_dtype) || !is_float_dtype(out_dtype))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "dequantize requires f32/bf16 parameters and output");
+  const int64_t per_word = 32 / static_cast<int64_t>(bits);
+  if (rows <= 0 || columns <= 0 || columns % per_word != 0 || columns % static_cast<int64_t>(group_size) != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "dequantize columns must divide into complete words and groups");
+  uint64_t count = 0;
+  if (!mul_ok(static_cast<uint64_t>(rows), static_cast<uint64_t>(columns), &count) || count > (uint64_t(1) << 60))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "dequantize size overflows");
+  if (packed == nullptr || scales == nullptr || biases == nullptr || out == nullptr)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "dequantize buffer is null");
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::dequantize_launch(packed, scales, biases, param_dtype, rows, columns, static_cast<int>(bits),
+                                          group_size, out, out_dtype, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "dequantize");
+  return AFFON_ROCM_OK;
+}
+
+// ---- host-pointer drop-in for compute_core_run_quantized_matmul_f32 ----
+
+namespace {
+
+std::mutex g_default_mutex;
+affon_rocm_session* g_default_session = nullptr;
+
+struct DeviceBuffer {
+  affon_rocm_session* session;
+  void* ptr = nullptr;
+  explicit DeviceBuffer(affon_rocm_session* s) : session(s) {}
+  ~DeviceBuffer() {
+    if (ptr != nullptr) {
+      hipSetDevice(session->device);
+      hipFree(ptr);
+    }
+  }
+};
+
+}  // namespace
+
+int compute_core_run_quantized_matmul_f32(const float* activation, size_t activation_count, const uint32_t* weights,
+                                          size_t weight_count, const float* scales, size_t scale_count,
+                                          const float* biases, size_t bias_count, float* output, size_t output_count,
+                                          size_t rows, size_t depth, size_t columns, size_t bits,
+                                          size_t group_size) {
+  clear_error();
+  // compute_core_cyna.zig:1012-1022, in the same order.
+  if (rows == 0 || depth == 0 || columns == 0 || group_size == 0 || (bits != 2 && bits != 4 && bits != 8))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "invalid quantized matmul shape");
+  const size_t per_word = 32 / bits;
+  if (depth % per_word != 0 || depth % group_size != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "depth must divide into complete words and groups");
+  uint64_t a_count = 0, w_count = 0, g_count = 0, o_count = 0;
+  if (!mul_ok(rows, depth, &a_count) || !mul_ok(columns, depth / per_word, &w_count) ||
+      !mul_ok(columns, depth / group_size, &g_count) || !mul_ok(rows, columns, &o_count))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized matmul counts overflow");
+  if (activation_count != a_count || weight_count != w_count || scale_count != g_count || bias_count != g_count ||
+      output_count != o_count)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized matmul buffer counts do not match the shape");
+  if (activation == nullptr || weights == nullptr || scales == nullptr || biases == nullptr || output == nullptr)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized matmul buffer is null");
+  uint64_t a_bytes, w_bytes, g_bytes, o_bytes;
+  if (!mul_ok(a_count, 4, &a_bytes) || !mul_ok(w_count, 4, &w_bytes) || !mul_ok(g_count, 4, &g_bytes) ||
+      !mul_ok(o_count, 4, &o_bytes))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "quantized matmul byte counts overflow");
+
+  std::lock_guard<std::mutex> lock(g_default_mutex);
+  if (g_default_session == nullptr) {
+    int status = affon_rocm_session_create(0, &g_default_session);
+    if (status != AFFON_ROCM_OK) {
+      g_default_session = nullptr;
+      return AFFON_ROCM_CORE_FAILURE;
+    }
+  }
+  affon_rocm_session* s = g_default_session;
+  DeviceBuffer dx(s), dw(s), ds(s), db(s), dout(s);
+  int status;
+  if ((status = affon_rocm_alloc(s, a_bytes, &dx.ptr)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_alloc(s, w_bytes, &dw.ptr)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_alloc(s, g_bytes, &ds.ptr)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_alloc(s, g_bytes, &db.ptr)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_alloc(s, o_bytes, &dout.ptr)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_memcpy_h2d(s, dx.ptr, activation, a_bytes)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_memcpy_h2d(s, dw.ptr, weights, w_bytes)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_memcpy_h2d(s, ds.ptr, scales, g_bytes)) != AFFON_ROCM_OK ||
+      (status = affon_rocm_memcpy_h2d(s, db.ptr, biases, g_bytes)) != AFFON_ROCM_OK)
+    return AFFON_ROCM_CORE_FAILURE;
+  const int64_t K = static_cast<int64_t>(depth), N = static_cast<int64_t>(columns), M = static_cast<int64_t>(rows);
+  const int64_t KW = K / static_cast<int64_t>(per_word), G = K / static_cast<int64_t>(group_size);
+  affon_rocm_qmm_desc d{};
+  d.input = {dx.ptr, a_bytes, 0, {M, K}, {K, 1}, AFFON_ROCM_F32};
+  d.packed = {dw.ptr, w_bytes, 0, {N, KW}, {KW, 1}, AFFON_ROCM_U32};
+  d.scales = {ds.ptr, g_bytes, 0, {N, G}, {G, 1}, AFFON_ROCM_F32};
+  d.biases = {db.ptr, g_bytes, 0, {N, G}, {G, 1}, AFFON_ROCM_F32};
+  d.output = static_cast<float*>(dout.ptr);
+  d.output_bytes = o_bytes;
+  d.bits = static_cast<uint32_t>(bits);
+  d.group_size = static_cast<uint32_t>(group_size);
+  d.implementation = AFFON_ROCM_IMPL_AUTO;
+  d.numerical_policy = AFFON_ROCM_BACKEND_EQUIVALENT;
+  if ((status = affon_rocm_quantized_matmul(s, &d)) != AFFON_ROCM_OK) return status == 1 ? 1 : AFFON_ROCM_CORE_FAILURE;
+  if ((status = affon_rocm_memcpy_d2h(s, output, dout.ptr, o_bytes)) != AFFON_ROCM_OK) return AFFON_ROCM_CORE_FAILURE;
+  return AFFON_ROCM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Internal interfaces between the C ABI (abi.cpp) and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#include "affon_rocm.h"
+
+namespace affon {
+
+// A validated quantized_matmul problem. Pointers already include the byte
+// offset of logical element [0,0]; strides are in elements.
+struct QmmProblem {
+  int64_t M = 0, N = 0, K = 0;
+  int bits = 0;
+  int64_t group = 0;
+  const uint8_t* x = nullptr;
+  int64_t xs0 = 0, xs1 = 0;
+  int x_dtype = AFFON_ROCM_F32;
+  const uint32_t* w = nullptr;
+  int64_t ws0 = 0, ws1 = 0;
+  const uint8_t* s = nullptr;
+  int64_t ss0 = 0, ss1 = 0;
+  const uint8_t* b = nullptr;
+  int64_t bs0 = 0, bs1 = 0;
+  int p_dtype = AFFON_ROCM_F32;
+  float* out = nullptr;
+};
+
+// Per-candidate capability guards and launchers. A guard returns true when
+// the candidate can run the problem (shape, layout, alignment); launchers
+// enqueue on the given stream and return the launch status.
+bool generic_supports(const QmmProblem& p);
+hipError_t generic_launch(const QmmProblem& p, hipStream_t stream);
+
+bool gemv_supports(const QmmProblem& p);
+hipError_t gemv_launch(const QmmProblem& p, hipStream_t stream);
+
+bool gemv_mfma_supports(const QmmProblem& p);
+hipError_t gemv_mfma_launch(const QmmProblem& p, hipStream_t stream);
+
+bool mfma_supports(const QmmProblem& p);
+hipError_t mfma_launch(const QmmProblem& p, hipStream_t stream);
+
+hipError_t quantize_launch(const void* weights, int weight_dtype, int64_t rows, int64_t columns,
+                           int bits, int64_t group, uint32_t* packed, void* scales, void* biases,
+                           int param_dtype, hipStream_t stream);
+hipError_t dequantize_launch(const uint32_t* packed, const void* scales, const void* biases,
+                             int param_dtype, int64_t rows, int64_t columns, int bits, int64_t group,
+                             void* out, int out_dtype, hipStream_t stream);
+
+}  // namespace affon

@@ -1,0 +1,238 @@
+"""``affon:ops`` subset for the weight-quantized linear path on the rocm device.
+
+``quantized_matmul`` mirrors src/js/ops.ts:69-79 and the formal validation of
+src/js/compute/program.ts:481-494 (same checks, same TypeError messages):
+four rank-two operands, f32/bf16 input, u32 packed weights, matching f32/bf16
+scales and biases, bits in {2, 4, 8}, a positive integer group_size, K divisible
+into whole words and groups, exact packed and parameter shapes; the result is
+f32 [M, N]. Evaluated operands run immediately on the Session's stream;
+formal operands add a node to the Program being built.
+
+``quantize`` and ``dequantize`` have no counterpart op in the reference (it
+packs only in test harnesses and states dequantization as a formula,
+docs/core/quantized-inference.md:59-61); they produce and expand the same
+packed format.
+
+``transpose`` and ``slice`` create strided views without copying, as the
+reference's view ops do for evaluated tensors.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Mapping, Sequence
+
+from . import _native
+from .core import FormalTensor, Tensor, TensorSpec, policy_code
+
+_IMPLEMENTATIONS = {
+    "auto": _native.IMPL_AUTO,
+    "generic": _native.IMPL_GENERIC,
+    "gemv": _native.IMPL_GEMV,
+    "gemv_mfma": _native.IMPL_GEMV_MFMA,
+    "mfma": _native.IMPL_MFMA,
+}
+
+
+def _options(options: Any, bits: Any, group_size: Any) -> dict[str, Any]:
+    if options is None:
+        options = {"bits": bits, "group_size": group_size}
+    elif not isinstance(options, Mapping):
+        raise TypeError("quantized_matmul options must be an object")
+    return dict(options)
+
+
+def _validate(specs: Sequence[TensorSpec], config: Mapping[str, Any]) -> TensorSpec:
+    """src/js/compute/program.ts:483-493, message for message."""
+    bits = config.get("bits") if config else None
+    if not config or bits not in (2, 4, 8) or isinstance(bits, bool):
+        raise TypeError("quantized_matmul bits must be 2, 4, or 8")
+    group = config.get("group_size")
+    if not isinstance(group, int) or isinstance(group, bool) or group <= 0:
+        raise TypeError("quantized_matmul group_size must be a positive integer")
+    if len(specs) != 4 or any(len(s.shape) != 2 for s in specs):
+        raise TypeError("quantized_matmul requires four rank-two tensors")
+    x, w, s, b = specs
+    if x.dtype not in ("f32", "bf16") or w.dtype != "u32" or s.dtype not in ("f32", "bf16") or b.dtype != s.dtype:
+        raise TypeError("quantized_matmul requires f32/bf16 input, u32 weights, and matching f32/bf16 scales and biases")
+    rows, inner = x.shape
+    outputs = w.shape[0]
+    per_word = 32 // bits
+    if (not rows or not inner or not outputs or inner % per_word or inner % group or
+            w.shape[1] != inner // per_word or s.shape[0] != outputs or s.shape[1] != inner // group or
+            b.shape[0] != outputs or b.shape[1] != inner // group):
+        raise TypeError("quantized_matmul packed or group dimensions do not match input features")
+    return TensorSpec("f32", (rows, outputs))
+
+
+def quantized_matmul(input: Any, packed: Any, scales: Any, biases: Any, options: Mapping[str, Any] | None = None,
+                     *, bits: int | None = None, group_size: int | None = None) -> Any:
+    """Y[M,N] = input[M,K] . dequant(packed, scales, biases)^T with f32 accumulation."""
+    operands = (input, packed, scales, biases)
+    config = _options(options, bits, group_size)
+    formal = [isinstance(o, FormalTensor) for o in operands]
+    if any(formal) and not all(formal):
+        raise TypeError("quantized_matmul cannot mix formal and evaluated tensors")
+    if all(formal):
+        builder = operands[0].builder
+        if any(o.builder is not builder for o in operands):
+            raise TypeError("quantized_matmul operands must belong to the same Program")
+        result = _validate([o.spec for o in operands], config)
+        return builder.emit("quantized_matmul", operands, result,
+                            {"bits": config["bits"], "group_size": config["group_size"]})
+    if not all(isinstance(o, Tensor) for o in operands):
+        raise TypeError("quantized_matmul requires tensors")
+    session = operands[0].session
+    if any(o.session is not session for o in operands):
+        raise TypeError("quantized_matmul operands must belong to the same Session")
+    _validate([o.spec for o in operands], config)
+    return _run_quantized_matmul(*operands, config["bits"], config["group_size"])
+
+
+def _descriptor(x: Tensor, w: Tensor, s: Tensor, b: Tensor, bits: int, group: int, out: Tensor | None,
+                implementation: str, policy: str) -> _native.QmmDesc:
+    desc = _native.QmmDesc()
+    desc.input, desc.packed, desc.scales, desc.biases = x.view(), w.view(), s.view(), b.view()
+    if out is not None:
+        desc.output = out.data_ptr
+        desc.output_bytes = out._buffer.nbytes - out.offset * 4
+    desc.bits = bits
+    desc.group_size = group
+    desc.implementation = _IMPLEMENTATIONS[implementation]
+    desc.numerical_policy = policy_code(policy)
+    return desc
+
+
+def _run_quantized_matmul(x: Tensor, w: Tensor, s: Tensor, b: Tensor, bits: int, group: int, *,
+                          policy: str = "backend_equivalent", implementation: str = "auto",
+                          out: Tensor | None = None) -> Tensor:
+    session = x.session
+    if out is None:
+        out = session.empty("f32", (x.shape[0], w.shape[0]))
+    desc = _descriptor(x, w, s, b, bits, group, out, implementation, policy)
+    _native.check(_native.load().affon_rocm_quantized_matmul(session._handle, ctypes.byref(desc)),
+                  "Program execution failed")
+    return out
+
+
+def quantized_matmul_into(out: Tensor, input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, *,
+                          bits: int, group_size: int, implementation: str = "auto",
+                          policy: str = "backend_equivalent") -> Tensor:
+    """Runs into a caller-owned f32 [M,N] output (no allocation), optionally
+    forcing one physical implementation."""
+    _validate([t.spec for t in (input, packed, scales, biases)], {"bits": bits, "group_size": group_size})
+    if out.dtype != "f32" or out.shape != (input.shape[0], packed.shape[0]) or not out.is_contiguous():
+        raise TypeError("quantized_matmul output must be a contiguous f32 [M,N] tensor")
+    return _run_quantized_matmul(input, packed, scales, biases, bits, group_size, policy=policy,
+                                 implementation=implementation, out=out)
+
+
+def selected_implementation(input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, *, bits: int,
+                            group_size: int, implementation: str = "auto",
+                            policy: str = "backend_equivalent") -> str:
+    desc = _descriptor(input, packed, scales, biases, bits, group_size, None, implementation, policy)
+    # Selection validates the output too; describe a conforming one.
+    desc.output = 1
+    desc.output_bytes = input.shape[0] * packed.shape[0] * 4
+    name = ctypes.create_string_buffer(128)
+    _native.check(_native.load().affon_rocm_quantized_matmul_select(ctypes.byref(desc), name, 128), "select")
+    return name.value.decode()
+
+
+def select_for_specs(specs: Sequence[TensorSpec], options: Mapping[str, Any], policy: str) -> str:
+    """Compile-time selection from formal specs: dense row-major operands at
+    an aligned base, as a Program's arguments are when run."""
+    _validate(specs, options)
+    desc = _native.QmmDesc()
+    views = []
+    for spec in specs:
+        rows, cols = spec.shape
+        itemsize = 2 if spec.dtype == "bf16" else 4
+        code = {"f32": _native.F32, "bf16": _native.BF16, "u32": _native.U32}[spec.dtype]
+        views.append(_native.View(256, rows * cols * itemsize, 0, (ctypes.c_int64 * 2)(rows, cols),
+                                  (ctypes.c_int64 * 2)(cols, 1), code))
+    desc.input, desc.packed, desc.scales, desc.biases = views
+    desc.output = 256
+    desc.output_bytes = specs[0].shape[0] * specs[1].shape[0] * 4
+    desc.bits = options["bits"]
+    desc.group_size = options["group_size"]
+    desc.implementation = _native.IMPL_AUTO
+    desc.numerical_policy = policy_code(policy)
+    name = ctypes.create_string_buffer(128)
+    status = _native.load().affon_rocm_quantized_matmul_select(ctypes.byref(desc), name, 128)
+    if status != _native.OK:
+        raise TypeError(f"no rocm quantized_matmul implementation: {_native.last_error()}")
+    return name.value.decode()
+
+
+def quantize(weights: Tensor, *, bits: int, group_size: int, param_dtype: str = "bf16") -> tuple[Tensor, Tensor, Tensor]:
+    """Affine group-wise quantize of a contiguous [N,K] f32/bf16 tensor into
+    (packed u32 [N,K/P], scales [N,K/g], biases [N,K/g])."""
+    if weights.dtype not in ("f32", "bf16") or len(weights.shape) != 2 or not weights.is_contiguous():
+        raise TypeError("quantize requires a contiguous rank-two f32/bf16 tensor")
+    if bits not in (2, 4, 8):
+        raise TypeError("quantize bits must be 2, 4, or 8")
+    if not isinstance(group_size, int) or group_size <= 0:
+        raise TypeError("quantize group_size must be a positive integer")
+    if param_dtype not in ("f32", "bf16"):
+        raise TypeError("quantize parameters must be f32 or bf16")
+    rows, cols = weights.shape
+    per_word = 32 // bits
+    if cols % per_word or cols % group_size:
+        raise TypeError("quantize columns must divide into complete words and groups")
+    session = weights.session
+    packed = session.empty("u32", (rows, cols // per_word))
+    scales = session.empty(param_dtype, (rows, cols // group_size))
+    biases = session.empty(param_dtype, (rows, cols // group_size))
+    code = {"f32": _native.F32, "bf16": _native.BF16}
+    _native.check(_native.load().affon_rocm_quantize(
+        session._handle, weights.data_ptr, code[weights.dtype], rows, cols, bits, group_size, packed.data_ptr,
+        scales.data_ptr, biases.data_ptr, code[param_dtype]), "quantize")
+    return packed, scales, biases
+
+
+def dequantize(packed: Tensor, scales: Tensor, biases: Tensor, *, bits: int, group_size: int,
+               dtype: str = "f32") -> Tensor:
+    """Expands packed weights to a [N,K] f32/bf16 tensor: w = s*q + b."""
+    for t in (packed, scales, biases):
+        if len(t.shape) != 2 or not t.is_contiguous():
+            raise TypeError("dequantize requires contiguous rank-two tensors")
+    if packed.dtype != "u32" or scales.dtype not in ("f32", "bf16") or biases.dtype != scales.dtype:
+        raise TypeError("dequantize requires u32 packed weights and matching f32/bf16 scales and biases")
+    if bits not in (2, 4, 8):
+        raise TypeError("dequantize bits must be 2, 4, or 8")
+    if not isinstance(group_size, int) or group_size <= 0:
+        raise TypeError("dequantize group_size must be a positive integer")
+    if dtype not in ("f32", "bf16"):
+        raise TypeError("dequantize output must be f32 or bf16")
+    rows = packed.shape[0]
+    cols = packed.shape[1] * (32 // bits)
+    if cols % group_size or scales.shape != (rows, cols // group_size) or biases.shape != scales.shape:
+        raise TypeError("dequantize parameter dimensions do not match the packed weights")
+    session = packed.session
+    out = session.empty(dtype, (rows, cols))
+    code = {"f32": _native.F32, "bf16": _native.BF16}
+    _native.check(_native.load().affon_rocm_dequantize(
+        session._handle, packed.data_ptr, scales.data_ptr, biases.data_ptr, code[scales.dtype], rows, cols, bits,
+        group_size, out.data_ptr, code[dtype]), "dequantize")
+    return out
+
+
+def transpose(t: Tensor, permutation: Sequence[int]) -> Tensor:
+    if sorted(permutation) != list(range(len(t.shape))):
+        raise TypeError("transpose permutation must list every axis once")
+    return Tensor(t.session, t._buffer, t.dtype, [t.shape[p] for p in permutation],
+                  [t.strides[p] for p in permutation], t.offset)
+
+
+def slice(t: Tensor, ranges: Sequence[Mapping[str, int]]) -> Tensor:  # noqa: A001 - reference op name
+    if len(ranges) != len(t.shape):
+        raise TypeError("slice needs one range per axis")
+    shape, strides, offset = [], [], t.offset
+    for dim, stride, r in zip(t.shape, t.strides, ranges):
+        start, stop, step = int(r.get("start", 0)), int(r.get("stop", dim)), int(r.get("step", 1))
+        if not (0 <= start <= stop <= dim) or step <= 0:
+            raise TypeError("slice range out of bounds")
+        shape.append((stop - start + step - 1) // step)
+        strides.append(stride * step)
+        offset += start * stride
+    return Tensor(t.session, t._buffer, t.dtype, shape, strides, offset)

@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the rocm weight-quantized linear path on one MI355X.
+
+A step is one quantized_matmul launch over one batch of synthetic input with
+the inputs already resident in HBM. The reported workload is the decode batch
+GEMV at 8-bit group 64: W [14336, 4096] packed u32 with bf16 scales/biases,
+x bf16 [1, 4096] from Affon's seeded generator (x: seed 1 N(0,1); W: seed 2
+N(0,0.02), quantized on the GPU). The same run also measures the 8-bit M sweep
+{2,4,8,16}, the 4-bit group-64 headline GEMV at 14336x4096, the f32 4096x4096
+4-bit case and (when available) the M=512 prefill, each as an extra field.
+
+Timing: the K timed steps are captured once into a HIP graph on the session's
+stream and replayed; HIP events recorded on that stream bracket the replay, so
+the per-step time is the GPU's back-to-back launch period without host
+overhead. Weight sets are rotated (>= 9 sets, > 600 MB in total) so that the
+256 MB Infinity Cache cannot hold the working set.
+
+Prints one JSON line. --gpus N with N > 1 exits: this path runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import pathlib
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "quant matmul GB/s (M=1) & TFLOP/s (M=512); % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+ROTATION_BYTES = 600e6
+
+
+class Hip:
+    """The few HIP runtime calls the benchmark needs (events and graphs)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        vp, pvp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        sig = {
+            "hipEventCreate": [pvp], "hipEventRecord": [vp, vp], "hipEventSynchronize": [vp],
+            "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp], "hipEventDestroy": [vp],
+            "hipStreamBeginCapture": [vp, ctypes.c_int], "hipStreamEndCapture": [vp, pvp],
+            "hipGraphInstantiate": [pvp, vp, vp, ctypes.c_char_p, ctypes.c_size_t], "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp], "hipStreamSynchronize": [vp],
+        }
+        for name, args in sig.items():
+            fn = getattr(self.lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+
+    def check(self, status: int, what: str) -> None:
+        if status != 0:
+            raise RuntimeError(f"{what} failed with HIP status {status}")
+
+    def event(self) -> ctypes.c_void_p:
+        ev = ctypes.c_void_p()
+        self.check(self.lib.hipEventCreate(ctypes.byref(ev)), "hipEventCreate")
+        return ev
+
+
+def algorithmic_bytes(M, N, K, bits, group, xbytes, pbytes):
+    """N*K*bits/8 + 2*N*(K/g)*sizeof(param) + M*K*sizeof(x) + M*N*4."""
+    return N * K * bits // 8 + 2 * N * (K // group) * pbytes + M * K * xbytes + M * N * 4
+
+
+class Workload:
+    def __init__(self, session, name, M, N, K, bits, group, x_dtype="bf16", p_dtype="bf16", policy="backend_equivalent",
+                 w_dtype=None, seed_x=1, seed_w=2):
+        import affon_amd as A
+        from affon_amd import ops
+        self.session, self.name = session, name
+        self.M, self.N, self.K, self.bits, self.group = M, N, K, bits, group
+        self.x_dtype, self.p_dtype, self.policy = x_dtype, p_dtype, policy
+        xbytes = 2 if x_dtype == "bf16" else 4
+        pbytes = 2 if p_dtype == "bf16" else 4
+        self.bytes = algorithmic_bytes(M, N, K, bits, group, xbytes, pbytes)
+        self.flops = 2 * M * N * K
+        set_bytes = N * K * bits // 8 + 2 * N * (K // group) * pbytes
+        self.sets = max(9, math.ceil(ROTATION_BYTES / set_bytes))
+        self.x = session.randn((M, K), seed=seed_x, dtype=x_dtype)
+        w = session.randn((N, K), seed=seed_w, std=0.02, dtype=w_dtype or p_dtype)
+        packed, scales, biases = A.quantize(w, bits=bits, group_size=group, param_dtype=p_dtype)
+        del w
+        self.weights = [(packed, scales, biases)]
+        for _ in range(self.sets - 1):
+            copies = []
+            for t in (packed, scales, biases):
+                c = session.empty(t.dtype, t.shape)
+                ops._native.check(ops._native.load().affon_rocm_memcpy_d2d(
+                    session._handle, c.data_ptr, t.data_ptr, c._buffer.nbytes), "copy")
+                copies.append(c)
+            self.weights.append(tuple(copies))
+        self.out = session.empty("f32", (M, N))
+        self.implementation = A.selected_implementation(self.x, packed, scales, biases, bits=bits, group_size=group,
+                                                        policy=policy)
+        self.descs = [ops._descriptor(self.x, w_, s_, b_, bits, group, self.out, "auto", policy)
+                      for (w_, s_, b_) in self.weights]
+        self.lib = ops._native.load()
+
+    def launch(self, i: int) -> None:
+        status = self.lib.affon_rocm_quantized_matmul(self.session._handle, ctypes.byref(self.descs[i % self.sets]))
+        if status != 0:
+            from affon_amd import _native
+            raise RuntimeError(_native.last_error())
+
+    def time(self, hip: Hip, steps: int, warmup: int, use_graph: bool = True) -> float:
+        """Returns milliseconds per step over `steps` back-to-back launches."""
+        stream = ctypes.c_void_p(self.session.stream)
+        for i in range(warmup):
+            self.launch(i)
+        self.session.synchronize()
+        start, stop = hip.event(), hip.event()
+        if use_graph:
+            graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+            hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed
+            for i in range(steps):
+                self.launch(i)
+            hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+            hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+            hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")  # untimed replay
+            self.session.synchronize()
+            hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+            hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+            hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+        else:
+            hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+            for i in range(steps):
+                self.launch(i)
+            hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+        hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+        self.session.synchronize()
+        ms = ctypes.c_float()
+        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+        if use_graph:
+            hip.lib.hipGraphExecDestroy(exe)
+            hip.lib.hipGraphDestroy(graph)
+        hip.lib.hipEventDestroy(start)
+        hip.lib.hipEventDestroy(stop)
+        return ms.value / steps
+
+    def host_operands(self):
+        packed, scales, biases = self.weights[0]
+        return self.x.storage(), packed.storage(), scales.storage(), biases.storage()
+
+    def release(self) -> None:
+        self.weights.clear()
+        self.descs.clear()
+
+
+def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0) -> dict:
+    """The oracle (the restated scalar CPU kernel) timed on this host, single
+    threaded as the reference's CPU kernel is (AFFON_CPU_THREADS=1), over a
+    bounded sample of output rows; also checks those rows against the GPU."""
+    from oracle import oracle as O
+    x, packed, scales, biases = work.host_operands()
+    M, N, K = work.M, work.N, work.K
+    probe = min(N, 64)
+    t0 = time.perf_counter()
+    O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, probe))
+    per_row = (time.perf_counter() - t0) / probe
+    rows = int(min(N, max(probe, seconds / max(per_row, 1e-9))))
+    t0 = time.perf_counter()
+    ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, rows))
+    elapsed = time.perf_counter() - t0
+    xbytes = 2 if work.x_dtype == "bf16" else 4
+    pbytes = 2 if work.p_dtype == "bf16" else 4
+    sample_bytes = algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
+    err = float(np.abs(gpu_out[:, :rows].astype(np.float64) - ref[:, :rows]).max())
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"value": round(sample_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle scalar quantized_matmul, rows 0..{rows} of {N} ({rows / N:.1%}) of the timed "
+                      f"workload, {elapsed:.1f} s on 1 thread; host {cpu}, nproc {os.cpu_count()}",
+            "max_abs_err_vs_gpu": err}
+
+
+def roofline_gemv(work: Workload, ms: float, traffic) -> dict:
+    achieved = work.bytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+def load_traffic(name: str):
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get(name)
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--launch", choices=["graph", "stream"], default="graph")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--only", default="", help="comma-separated subset of extra workloads to run")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the quantized linear path has no multi-GPU execution "
+              f"(requested --gpus {args.gpus})", file=sys.stderr)
+        return 2
+
+    import affon_amd as A
+    hip = Hip()
+    session = A.Session("rocm")
+    use_graph = args.launch == "graph"
+
+    main_work = Workload(session, "decode_8bit_g64_m1", 1, 14336, 4096, 8, 64)
+    ms = main_work.time(hip, args.steps, args.warmup, use_graph)
+    gpu_out = main_work.out.numpy()
+    value = main_work.bytes / (ms * 1e-3) / 1e9
+    roofline = roofline_gemv(main_work, ms, load_traffic(main_work.name))
+    impl = main_work.implementation
+    sets = main_work.sets
+    baseline = cpu_baseline(main_work, gpu_out, args.cpu_seconds)
+    main_work.release()
+
+    extras = {}
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not only or name in only
+
+    def record(name, work, bound="hbm"):
+        t = work.time(hip, args.steps, args.warmup, use_graph)
+        entry = {"implementation": work.implementation, "us_per_step": round(t * 1e3, 3),
+                 "GB/s": round(work.bytes / (t * 1e-3) / 1e9, 1),
+                 "TFLOP/s": round(work.flops / (t * 1e-3) / 1e12, 3)}
+        if bound == "hbm":
+            entry["hbm_frac"] = round(entry["GB/s"] / HBM_PEAK_GBS, 4)
+        else:
+            entry["mfma_frac"] = round(entry["TFLOP/s"] / BF16_MFMA_PEAK_TFLOPS, 4)
+        extras[name] = entry
+        work.release()
+
+    for M in (2, 4, 8, 16):
+        if want(f"decode_8bit_g64_m{M}"):
+            record(f"decode_8bit_g64_m{M}", Workload(session, f"decode_8bit_g64_m{M}", M, 14336, 4096, 8, 64))
+    if want("decode_4bit_g64_m1"):
+        record("decode_4bit_g64_m1", Workload(session, "decode_4bit_g64_m1", 1, 14336, 4096, 4, 64))
+    if want("decode_4bit_g64_f32_4096"):
+        record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
+                                                    x_dtype="f32", p_dtype="f32"))
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (Affon seeded generator: x seed 1 N(0,1) bf16, W seed 2 N(0,0.02) quantized on GPU)",
+        "config": {"workload": "decode GEMV 8-bit group 64, W[14336,4096] u32-packed with bf16 scales/biases, "
+                               "x bf16 [1,4096], f32 out", "M": 1, "N": 14336, "K": 4096, "bits": 8,
+                   "group_size": 64, "implementation": impl, "launch": args.launch,
+                   "weight_sets_rotated": sets},
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+        "extra": extras,
+    }
+    print(json.dumps(result), flush=True)
+    session.dispose()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
