@@ -12,6 +12,10 @@
 #include "device.h"
 #include "internal.h"
 
+// Products and sums must stay separately rounded (this file is also built
+// with -ffp-contract=off).
+#pragma clang fp contract(off)
+
 namespace affon {
 namespace {
 
@@ -34,8 +38,8 @@ __global__ __launch_bounds__(256) void qmm_generic_kernel(QmmProblem p) {
     const int64_t g = k / p.group;
     const float s = PT::load(p.s, n * p.ss0 + g * p.ss1);
     const float b = PT::load(p.b, n * p.bs0 + g * p.bs1);
-    const float w = __fadd_rn(__fmul_rn(s, static_cast<float>(q)), b);
-    acc = __fadd_rn(acc, __fmul_rn(XT::load(xrow, k * p.xs1), w));
+    const float w = s * static_cast<float>(q) + b;
+    acc = acc + XT::load(xrow, k * p.xs1) * w;
   }
   p.out[m * p.N + n] = acc;
 }

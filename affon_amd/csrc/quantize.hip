@@ -12,6 +12,8 @@
 #include "device.h"
 #include "internal.h"
 
+// No fused multiply-add anywhere in this file (also built with
+// -ffp-contract=off): dequantization rounds the product and the sum separately.
 #pragma clang fp contract(off)
 
 namespace affon {
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* packed,
     const int64_t g = e / group;
     const float s = load_param<PT>(scales, g);
     const float b = load_param<PT>(biases, g);
-    const float w = __fadd_rn(__fmul_rn(s, static_cast<float>((word >> (i * bits)) & mask)), b);
+    const float w = s * static_cast<float>((word >> (i * bits)) & mask) + b;
     if constexpr (OT::bytes == 2)
       static_cast<uint16_t*>(out)[e] = f32_to_bf16_bits(w);
     else

@@ -268,6 +268,22 @@ def test_seeded_random_every_implementation(session, bits, group, x_dtype, p_dty
             check_against_oracle(out, x, packed, s, b, bits, group, x_dtype == "bf16")
 
 
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 32), (2, 16), (4, 3)])
+@pytest.mark.parametrize("x_dtype,p_dtype", [("f32", "f32"), ("bf16", "bf16")])
+def test_generic_is_bit_identical_to_ordered_cpu_loop(session, bits, group, x_dtype, p_dtype):
+    """The exact-class candidate (the only one exact_only admits) reproduces the
+    ordered, separately rounded f32 loop bit for bit on non-dyadic data."""
+    K = int(np.lcm(32 // bits, group)) * 16
+    x, packed, s, b = seeded_problem(3, 50, K, bits, group, x_dtype, p_dtype, seed=4)
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    out = session.empty("f32", (3, 50))
+    A.quantized_matmul_into(out, xt, wt, st, bt, bits=bits, group_size=group, implementation="generic")
+    np.testing.assert_array_equal(out.numpy(), O.quantized_matmul(x, packed, s, b, bits, group))
+    exact = session.empty("f32", (3, 50))
+    A.quantized_matmul_into(exact, xt, wt, st, bt, bits=bits, group_size=group, policy="exact_only")
+    np.testing.assert_array_equal(exact.numpy(), out.numpy())
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_decode_sweep_full_size(session, M):
     """8-bit group-64 decode sweep at 14336x4096, bf16 operands, full output."""
