@@ -17,6 +17,7 @@
 //     shuffles, and across K-parts (waves of one block) through LDS.
 
 #include "device.h"
+#include "gemv1_dispatch.h"
 #include "internal.h"
 
 namespace affon {
@@ -257,7 +258,30 @@ bool gemv_supports(const QmmProblem& p) {
   return true;
 }
 
+bool gemv1_supports(const QmmProblem& p) {
+  // One activation row, dense rows, 16-byte aligned packed rows and
+  // activations, every 16-byte chunk inside one group, LDS for the row.
+  const int64_t cv = 128 / p.bits;
+  const int xbytes = p.x_dtype == AFFON_ROCM_BF16 ? 2 : 4;
+  if (p.M != 1 || p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
+  if (p.K % cv != 0 || p.group % cv != 0) return false;
+  const int64_t chunks_per_group = p.group / cv;
+  if ((chunks_per_group & (chunks_per_group - 1)) != 0) return false;  // group index by shift
+  if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0 || p.ws0 % 4 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return false;
+  const int64_t chunks = p.K / cv;
+  const int64_t lds = (chunks * (cv * xbytes / 4 + 1) + 4) * 4;
+  return lds <= gemv1::kMaxLdsBytes && chunks <= gemv1::kMaxChunks;
+}
+
 hipError_t gemv_launch(const QmmProblem& p, hipStream_t stream) {
+  if (gemv1_supports(p)) {
+    switch (p.bits) {
+      case 2: return gemv1_launch_b2(p, stream);
+      case 4: return gemv1_launch_b4(p, stream);
+      default: return gemv1_launch_b8(p, stream);
+    }
+  }
   switch (p.bits) {
     case 2: return launch_bits<2>(p, stream);
     case 4: return launch_bits<4>(p, stream);

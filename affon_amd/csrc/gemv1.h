@@ -1,0 +1,349 @@
+// Single-row decode kernel (M = 1) of rocm_quantized_matmul.gemv.
+//
+// The decode GEMV is a pure stream over the packed weights (0.5 or 1 byte
+// per weight), so the kernel is organised to keep as many bytes in flight as
+// possible and to spend as few VALU instructions per weight as the exact
+// arithmetic allows:
+//   * a wave owns R output rows and a K-part of every row; each lane owns
+//     CPL 16-byte chunks (4 packed words) per row, chunk c = part_base + lane
+//     + 64*i, so one load instruction reads 1 KiB of contiguous packed words
+//     of one row; all R*CPL chunk loads (and the group parameters) are issued
+//     before anything waits;
+//   * the activation row is staged once per workgroup in LDS together with
+//     the sum of every chunk's activations; each wave copies its chunks into
+//     registers once and reuses them for its R rows;
+//   * codes are converted exactly (FP8 conversions for 2/4-bit codes,
+//     v_cvt_f32_ubyte for 8-bit codes) and multiplied with v_dot2_f32_bf16
+//     (bf16 x) or v_fma_f32 (f32 x); each chunk lies inside one group, so its
+//     parameters are applied once per chunk: y += s * sum(x*q) + b * sum(x);
+//   * rows are reduced across the wave with butterfly shuffles and across the
+//     K-parts of a workgroup through LDS.
+#pragma once
+
+#include "device.h"
+#include "internal.h"
+
+namespace affon {
+namespace gemv1 {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+struct Args {
+  const uint32_t* w;
+  int64_t ws0;  // packed row stride in words
+  const uint8_t* s;
+  int64_t ss0;
+  const uint8_t* b;
+  int64_t bs0;
+  const uint8_t* x;
+  float* out;
+  int64_t N;
+  int cpg_shift;  // log2(16-byte chunks per group)
+  int chunks;  // 16-byte chunks per row
+  int part;    // chunks per K-part
+  int ks;      // K-parts per row (waves per row block)
+};
+
+template <int BITS>
+constexpr int chunk_values() { return 128 / BITS; }
+
+__device__ __forceinline__ bf16x2_t pack2(float a, float b) { return bf16x2_t{static_cast<__bf16>(a), static_cast<__bf16>(b)}; }
+
+// Exact decoding of packed codes.
+//
+// 4-bit and 2-bit codes: a byte holding a code n < 16 read as an FP8 E4M3
+// value is exactly n * 2^-9 (the subnormal range and the first binade of E4M3
+// are evenly spaced by 2^-9), so one v_cvt_scalef32_pk_bf16_fp8 (bf16) or
+// v_cvt_pk_f32_fp8 (f32) turns two codes into exact operands. The unit is
+// measured in the kernel (fp8_unit) rather than assumed, and divided out of the
+// group scale. 8-bit codes use v_cvt_f32_ubyteN (one exact conversion each).
+//
+// Operand order: bf16 activations are staged in LDS in the pair order the
+// conversions produce (see stage_chunk), f32 activations in k order.
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bf16x2_t fp8_pair_bf16(uint32_t bytes, bool high) {
+  return high ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, 1.0f, true)
+              : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, 1.0f, false);
+}
+
+__device__ __forceinline__ f32x2_t fp8_pair_f32(uint32_t bytes, bool high) {
+  return high ? __builtin_amdgcn_cvt_pk_f32_fp8(bytes, true) : __builtin_amdgcn_cvt_pk_f32_fp8(bytes, false);
+}
+
+// Value of one code step after the FP8 conversion (2^-9 for OCP E4M3).
+template <typename XT>
+__device__ __forceinline__ float fp8_unit() {
+  if constexpr (XT::bytes == 2) {
+    const bf16x2_t v = fp8_pair_bf16(0x08u, false);
+    return static_cast<float>(v.x) * 0.125f;
+  } else {
+    return fp8_pair_f32(0x08u, false).x * 0.125f;
+  }
+}
+
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Bytes of one word holding codes in their low bits, and the k index (within
+// the word) of the code in byte j of mask t.
+//   4-bit: mask 0 = w & 0x0f0f0f0f (k = 2j), mask 1 = (w >> 4) & .. (k = 2j+1)
+//   2-bit: mask t = (w >> 2t) & 0x03030303 (k = 4j + t)
+template <int BITS>
+__device__ __forceinline__ int code_k(int t, int j) {
+  return BITS == 4 ? 2 * j + t : 4 * j + t;
+}
+
+// Sum over one 16-byte chunk (4 words) of x*q in units of the code step
+// (fp8 path) or exactly (8-bit path). xr holds the chunk's activations as
+// staged: bf16 pairs, or f32 values in k order.
+template <int BITS, typename XT>
+__device__ __forceinline__ float chunk_dot(const uint32_t* words, const uint32_t* xr) {
+  constexpr int P = 32 / BITS;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = words[i];
+    if constexpr (BITS == 8) {
+      const uint32_t v = opaque(w);
+      float q[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[j] = static_cast<float>((v >> (8 * j)) & 0xffu);
+      if constexpr (XT::bytes == 2) {
+        acc = __builtin_amdgcn_fdot2_f32_bf16(pack2(q[0], q[1]), __builtin_bit_cast(bf16x2_t, xr[2 * i]), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(pack2(q[2], q[3]), __builtin_bit_cast(bf16x2_t, xr[2 * i + 1]), acc,
+                                              false);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = fmaf(__uint_as_float(xr[4 * i + j]), q[j], acc);
+      }
+    } else {
+      constexpr int T = BITS == 4 ? 2 : 4;  // masks per word
+      constexpr uint32_t kMask = BITS == 4 ? 0x0f0f0f0fu : 0x03030303u;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint32_t m = (w >> (BITS * t)) & kMask;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (XT::bytes == 2) {
+            acc = __builtin_amdgcn_fdot2_f32_bf16(fp8_pair_bf16(m, h == 1),
+                                                  __builtin_bit_cast(bf16x2_t, xr[i * (P / 2) + 2 * t + h]), acc,
+                                                  false);
+          } else {
+            const f32x2_t q = fp8_pair_f32(m, h == 1);
+            acc = fmaf(__uint_as_float(xr[i * P + code_k<BITS>(t, 2 * h)]), q.x, acc);
+            acc = fmaf(__uint_as_float(xr[i * P + code_k<BITS>(t, 2 * h + 1)]), q.y, acc);
+          }
+        }
+      }
+    }
+  }
+  return acc;
+}
+
+// Writes one chunk of bf16 activations (src: CV values in k order) into the
+// pair order chunk_dot consumes and returns the sum of the chunk.
+template <int BITS>
+__device__ __forceinline__ void permute_bf16_chunk(const uint32_t* src, uint32_t* dst) {
+  constexpr int P = 32 / BITS;
+  auto value = [&](int k) -> uint32_t { return (src[k >> 1] >> (16 * (k & 1))) & 0xffffu; };
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = src[i];
+  } else {
+    constexpr int T = BITS == 4 ? 2 : 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k0 = i * P + code_k<BITS>(t, 2 * h);
+          const int k1 = i * P + code_k<BITS>(t, 2 * h + 1);
+          dst[i * (P / 2) + 2 * t + h] = value(k0) | (value(k1) << 16);
+        }
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum of v over the 64 lanes of the wave, returned in every lane: DPP adds
+// within rows of 16 (quad swaps, then row rotations by 4 and 8), then the
+// four row sums are read out of lanes 0, 16, 32 and 48.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x124>(v);  // row_ror:4
+  v += dpp<0x128>(v);  // row_ror:8
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+template <int BITS, typename XT, typename PT, int R, int CPL>
+__global__ __launch_bounds__(kThreads) void kernel(Args a) {
+  constexpr int CV = chunk_values<BITS>();
+  constexpr int XDW = CV * XT::bytes / 4;  // dwords of activations per chunk
+  // LDS: the activation row, slot-major (16-byte slot j of chunk c at
+  // uint4 index j*chunks + c, so lanes reading consecutive chunks hit
+  // consecutive banks), then one f32 sum per chunk, then the K-part partials.
+  extern __shared__ uint32_t smem[];
+  uint4* xs_lds = reinterpret_cast<uint4*>(smem);
+  float* xsum_lds = reinterpret_cast<float*>(smem + a.chunks * XDW);
+  float* red = xsum_lds + a.chunks;
+
+  // The wave index is uniform; reading it into a scalar register keeps all
+  // row addressing on the scalar unit.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int kp = wave % a.ks;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * R;
+  const int c_begin = kp * a.part;
+  const int c_end = min(a.chunks, c_begin + a.part);
+
+  // 1. Issue every packed-word and parameter load of this wave.
+  uint32_t wv[R][CPL][4];
+  float sv[R][CPL], bv[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // Row bases are wave-uniform (scalar registers); lane offsets are 32-bit.
+    const int64_t n = n0 + r < a.N ? n0 + r : a.N - 1;
+    const u32x4_t* row = reinterpret_cast<const u32x4_t*>(a.w + n * a.ws0);
+    const uint8_t* srow = a.s + n * a.ss0 * PT::bytes;
+    const uint8_t* brow = a.b + n * a.bs0 * PT::bytes;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = c_begin + lane + 64 * i;
+      const int cc = c < c_end ? c : 0;  // idle lanes read chunk 0 and discard it
+      const u32x4_t v = __builtin_nontemporal_load(row + cc);
+      wv[r][i][0] = v.x;
+      wv[r][i][1] = v.y;
+      wv[r][i][2] = v.z;
+      wv[r][i][3] = v.w;
+      const int g = cc >> a.cpg_shift;
+      sv[r][i] = PT::load(srow, g);
+      bv[r][i] = PT::load(brow, g);
+    }
+  }
+
+  // 2. Stage the activation row (bf16: in chunk_dot pair order) and the sum
+  //    of every chunk in LDS.
+  for (int c = threadIdx.x; c < a.chunks; c += kThreads) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(c) * CV * XT::bytes);
+    uint32_t raw[XDW];
+#pragma unroll
+    for (int i = 0; i < XDW / 4; ++i) {
+      const uint4 v = src[i];
+      raw[4 * i] = v.x;
+      raw[4 * i + 1] = v.y;
+      raw[4 * i + 2] = v.z;
+      raw[4 * i + 3] = v.w;
+    }
+    uint32_t staged[XDW];
+    float sum = 0.0f;
+    if constexpr (XT::bytes == 2) {
+      permute_bf16_chunk<BITS>(raw, staged);
+      const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+#pragma unroll
+      for (int i = 0; i < XDW; ++i)
+        sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, staged[i]), ones, sum, false);
+    } else {
+#pragma unroll
+      for (int i = 0; i < XDW; ++i) {
+        staged[i] = raw[i];
+        sum += __uint_as_float(raw[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < XDW / 4; ++i)
+      xs_lds[i * a.chunks + c] = make_uint4(staged[4 * i], staged[4 * i + 1], staged[4 * i + 2], staged[4 * i + 3]);
+    xsum_lds[c] = sum;
+  }
+  __syncthreads();
+
+  // 3. Decode, multiply, apply group parameters per chunk.
+  // Converted codes are n * unit; scales are divided by the unit (a power of
+  // two, so exactly).
+  const float inv_unit = BITS == 8 ? 1.0f : 1.0f / fp8_unit<XT>();
+  float y[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) y[r] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = c_begin + lane + 64 * i;
+    if (c < c_end) {
+      uint32_t xr[XDW];
+#pragma unroll
+      for (int j = 0; j < XDW / 4; ++j) {
+        const uint4 v = xs_lds[j * a.chunks + c];
+        xr[4 * j] = v.x;
+        xr[4 * j + 1] = v.y;
+        xr[4 * j + 2] = v.z;
+        xr[4 * j + 3] = v.w;
+      }
+      const float xsum = xsum_lds[c];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float acc = chunk_dot<BITS, XT>(wv[r][i], xr);
+        y[r] = fmaf(sv[r][i] * inv_unit, acc, fmaf(bv[r][i], xsum, y[r]));
+      }
+    }
+  }
+
+  // 4. Reduce across the wave, then across K-parts.
+#pragma unroll
+  for (int r = 0; r < R; ++r) y[r] = wave_sum(y[r]);
+  if (a.ks == 1) {
+    if (lane < R) {
+      float v = y[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r) v = lane == r ? y[r] : v;
+      if (n0 + lane < a.N) a.out[n0 + lane] = v;
+    }
+    return;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[wave * R + r] = y[r];
+  }
+  __syncthreads();
+  if (kp == 0 && lane < R) {
+    float v = 0.0f;
+    for (int j = 0; j < a.ks; ++j) v += red[(wave + j) * R + lane];
+    if (n0 + lane < a.N) a.out[n0 + lane] = v;
+  }
+}
+
+template <int BITS, typename XT, typename PT, int R, int CPL>
+hipError_t launch(const Args& a, hipStream_t stream) {
+  constexpr int CV = chunk_values<BITS>();
+  constexpr int XDW = CV * XT::bytes / 4;
+  const size_t lds = (static_cast<size_t>(a.chunks) * (XDW + 1) + kWaves * R) * 4;
+  const int64_t row_blocks = (a.N + R - 1) / R;
+  const int64_t per_block = kWaves / a.ks;
+  const unsigned blocks = static_cast<unsigned>((row_blocks + per_block - 1) / per_block);
+  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL>), dim3(blocks), dim3(kThreads), lds, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace gemv1
+
+// Per-bits entry points (one translation unit each).
+bool gemv1_supports(const QmmProblem& p);
+hipError_t gemv1_launch_b2(const QmmProblem& p, hipStream_t stream);
+hipError_t gemv1_launch_b4(const QmmProblem& p, hipStream_t stream);
+hipError_t gemv1_launch_b8(const QmmProblem& p, hipStream_t stream);
+
+}  // namespace affon

@@ -1,0 +1,9 @@
+// M = 1 decode kernels for 8-bit packed weights (one translation unit per
+// bit width so the variants compile in parallel).
+#include "gemv1_dispatch.h"
+
+namespace affon {
+
+hipError_t gemv1_launch_b8(const QmmProblem& p, hipStream_t stream) { return gemv1::dispatch_bits<8>(p, stream); }
+
+}  // namespace affon

@@ -1,0 +1,143 @@
+// Host-side shape selection for the M = 1 decode kernel.
+//
+// For every (R rows, CPL chunks per lane) variant the number of K-parts is the
+// smallest that gives each lane at most CPL chunks; the variant chosen is the
+// one that runs in the fewest rounds of resident waves (occupancy from the
+// compiled kernel), then with the fewest K-parts (no LDS reduction and
+// barrier), then with the most waves (more latency hiding). On MI355X this
+// picks the fastest or a variant within 6% of it on every decode shape of
+// the benchmark sweep (8/4-bit 14336x4096, 4096x14336, 4096x4096 f32,
+// 1024x4096, 128256x4096).
+#pragma once
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "gemv1.h"
+
+namespace affon {
+namespace gemv1 {
+
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+// Largest row the variants cover: 4 K-parts x 64 lanes x 4 chunks.
+constexpr int64_t kMaxChunks = 4 * 64 * 4;
+
+struct Variant {
+  int R;
+  int CPL;
+  hipError_t (*launch)(const Args&, hipStream_t);
+  const void* fn;
+  size_t (*lds)(int chunks);
+};
+
+template <int BITS, typename XT, int R>
+size_t lds_bytes(int chunks) {
+  constexpr int XDW = chunk_values<BITS>() * XT::bytes / 4;
+  return (static_cast<size_t>(chunks) * (XDW + 1) + kWaves * R) * 4;
+}
+
+template <int BITS, typename XT, typename PT>
+const Variant* variants(int* count) {
+#define AFFON_GEMV1_VARIANT(R, CPL)                                                                   \
+  {R, CPL, launch<BITS, XT, PT, R, CPL>, reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL>), \
+   lds_bytes<BITS, XT, R>}
+  static const Variant table[] = {
+      AFFON_GEMV1_VARIANT(1, 1), AFFON_GEMV1_VARIANT(2, 1), AFFON_GEMV1_VARIANT(4, 1), AFFON_GEMV1_VARIANT(8, 1),
+      AFFON_GEMV1_VARIANT(1, 2), AFFON_GEMV1_VARIANT(2, 2), AFFON_GEMV1_VARIANT(4, 2), AFFON_GEMV1_VARIANT(2, 4),
+      AFFON_GEMV1_VARIANT(4, 4),
+  };
+#undef AFFON_GEMV1_VARIANT
+  *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
+  return table;
+}
+
+inline int device_cus() {
+  static std::mutex mutex;
+  static int cached[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mutex);
+  if (cached[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
+    cached[device] = cus;
+  }
+  return cached[device];
+}
+
+// Resident blocks per CU of a compiled variant at a given LDS size (cached:
+// the query costs more than a launch).
+inline int blocks_per_cu(const void* fn, size_t lds) {
+  static std::mutex mutex;
+  static std::map<std::pair<const void*, size_t>, int> cache;
+  std::lock_guard<std::mutex> lock(mutex);
+  const auto key = std::make_pair(fn, lds);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, lds) != hipSuccess || blocks <= 0) blocks = 1;
+  cache.emplace(key, blocks);
+  return blocks;
+}
+
+template <int BITS, typename XT, typename PT>
+hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
+  Args a;
+  a.w = p.w;
+  a.ws0 = p.ws0;
+  a.s = p.s;
+  a.ss0 = p.ss0;
+  a.b = p.b;
+  a.bs0 = p.bs0;
+  a.x = p.x;
+  a.out = p.out;
+  a.N = p.N;
+  a.chunks = static_cast<int>(p.K * BITS / 128);
+  a.cpg_shift = 0;
+  while ((int64_t(1) << a.cpg_shift) * chunk_values<BITS>() < p.group) ++a.cpg_shift;
+  int count = 0;
+  const Variant* table = variants<BITS, XT, PT>(&count);
+  const int cus = device_cus();
+  const Variant* best = nullptr;
+  int best_ks = 0;
+  int64_t best_rounds = 0, best_waves = 0;
+  for (int i = 0; i < count; ++i) {
+    const Variant& v = table[i];
+    int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
+    if (ks == 3) ks = 4;
+    if (ks > 4) continue;
+    const int part = (a.chunks + ks - 1) / ks;
+    if (v.CPL > 1 && 64 * (v.CPL - 1) >= part) continue;  // a chunk slot would stay empty
+    const size_t lds = v.lds(a.chunks);
+    if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
+    const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
+    const int64_t waves = (p.N + v.R - 1) / v.R * ks;
+    const int64_t rounds = (waves + capacity - 1) / capacity;
+    const bool better = best == nullptr || rounds < best_rounds ||
+                        (rounds == best_rounds && (ks < best_ks || (ks == best_ks && waves > best_waves)));
+    if (better) {
+      best = &v;
+      best_ks = ks;
+      best_rounds = rounds;
+      best_waves = waves;
+    }
+  }
+  if (best == nullptr) return hipErrorInvalidValue;
+  a.ks = best_ks;
+  a.part = (a.chunks + best_ks - 1) / best_ks;
+  return best->launch(a, stream);
+}
+
+template <int BITS>
+hipError_t dispatch_bits(const QmmProblem& p, hipStream_t stream) {
+  if (p.x_dtype == AFFON_ROCM_BF16) {
+    if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, BF16, BF16>(p, stream);
+    return dispatch<BITS, BF16, F32>(p, stream);
+  }
+  if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, F32, BF16>(p, stream);
+  return dispatch<BITS, F32, F32>(p, stream);
+}
+
+}  // namespace gemv1
+}  // namespace affon

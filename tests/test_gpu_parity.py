@@ -284,6 +284,26 @@ def test_generic_is_bit_identical_to_ordered_cpu_loop(session, bits, group, x_dt
     np.testing.assert_array_equal(exact.numpy(), out.numpy())
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("x_dtype,p_dtype", [("bf16", "bf16"), ("f32", "f32"), ("bf16", "f32")])
+def test_decode_integer_products_exact(session, bits, x_dtype, p_dtype, rng):
+    """Integer activations, every code value, power-of-two scales and integer
+    biases make every product and partial sum exact in f32, so the decode
+    kernels must match exactly (shapes chosen so the M=1 kernel accepts them:
+    K a multiple of 128/bits, group a power-of-two number of 16-byte chunks)."""
+    for M, N, K, group in [(1, 37, 512, 64), (1, 130, 4096, 128), (1, 9, 14336, 64), (3, 40, 1024, 64)]:
+        q = rng.integers(0, 1 << bits, size=(N, K))
+        x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
+        s = 2.0 ** rng.integers(-2, 2, size=(N, K // group))
+        b = rng.integers(-2, 3, size=(N, K // group)).astype(np.float64)
+        expected = reference_f64(x, q, s, b, group)
+        xt = upload(session, storage(x, x_dtype), x_dtype)
+        wt = upload(session, pack_codes(q, bits), "u32")
+        st, bt = upload(session, storage(s, p_dtype), p_dtype), upload(session, storage(b, p_dtype), p_dtype)
+        for impl, out in run_all(session, xt, wt, st, bt, bits, group).items():
+            np.testing.assert_array_equal(out, expected.astype(np.float32), err_msg=f"{impl} {M}x{N}x{K} g{group}")
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_decode_sweep_full_size(session, M):
     """8-bit group-64 decode sweep at 14336x4096, bf16 operands, full output."""
