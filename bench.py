@@ -253,6 +253,11 @@ def main() -> int:
             record(f"decode_8bit_g64_m{M}", Workload(session, f"decode_8bit_g64_m{M}", M, 14336, 4096, 8, 64))
     if want("decode_4bit_g64_m1"):
         record("decode_4bit_g64_m1", Workload(session, "decode_4bit_g64_m1", 1, 14336, 4096, 4, 64))
+    for name, N, K in (("prefill_4bit_g64_m512_n14336_k4096", 14336, 4096),
+                       ("prefill_4bit_g64_m512_n4096_k14336", 4096, 14336)):
+        if want(name):
+            record(name, Workload(session, name, 512, N, K, 4, 64, policy="approximate"), bound="mfma")
+            extras[name]["numerical_policy"] = "approximate"
     if want("decode_4bit_g64_f32_4096"):
         record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
                                                     x_dtype="f32", p_dtype="f32"))

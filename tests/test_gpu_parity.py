@@ -323,6 +323,82 @@ def test_decode_headline_4bit_full_size(session):
     check_against_oracle(A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=64).numpy(), x, packed, s, b, 4, 64, False)
 
 
+# ---- prefill GEMM (decoded weights rounded to bf16: numerical class "approximate") ----
+
+def run_mfma(session, x, w, s, b, bits, group):
+    out = session.empty("f32", (x.shape[0], w.shape[0]))
+    A.quantized_matmul_into(out, x, w, s, b, bits=bits, group_size=group, implementation="mfma", policy="approximate")
+    return out.numpy()
+
+
+def test_prefill_selection_follows_policy(session):
+    x, packed, s, b = seeded_problem(64, 128, 256, 4, 64, "bf16", "bf16")
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=64, policy="approximate") == \
+        "rocm_quantized_matmul.mfma"
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=64) != "rocm_quantized_matmul.mfma"
+    out = session.empty("f32", (64, 128))
+    with pytest.raises(_native.NativeError, match="numerical policy"):
+        A.quantized_matmul_into(out, xt, wt, st, bt, bits=4, group_size=64, implementation="mfma")
+    # K not a multiple of 256: the prefill kernel declines, AUTO falls back.
+    x, packed, s, b = seeded_problem(64, 128, 192, 4, 64, "bf16", "bf16")
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    impl = A.selected_implementation(xt, wt, st, bt, bits=4, group_size=64, policy="approximate")
+    assert impl != "rocm_quantized_matmul.mfma"
+    y = session.empty("f32", (64, 128))
+    A.quantized_matmul_into(y, xt, wt, st, bt, bits=4, group_size=64, policy="approximate")
+    check_against_oracle(y.numpy(), x, packed, s, b, 4, 64, True)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("p_dtype", ["bf16", "f32"])
+def test_prefill_exact_integer_products(session, bits, p_dtype, rng):
+    """Power-of-two scales and zero biases keep every decoded weight exact in
+    bf16 and every partial sum exact in f32: the GEMM must match exactly,
+    including partial M/N tiles and one or many K steps."""
+    for M, N, K, group in [(64, 128, 256, 32), (100, 40, 512, 64), (300, 300, 1024, 128), (515, 129, 4096, 64)]:
+        q = rng.integers(0, 1 << bits, size=(N, K))
+        x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
+        s = 2.0 ** rng.integers(-3, 1, size=(N, K // group))
+        b = np.zeros((N, K // group))
+        expected = reference_f64(x, q, s, b, group)
+        xt = upload(session, storage(x, "bf16"), "bf16")
+        wt = upload(session, pack_codes(q, bits), "u32")
+        st, bt = upload(session, storage(s, p_dtype), p_dtype), upload(session, storage(b, p_dtype), p_dtype)
+        np.testing.assert_array_equal(run_mfma(session, xt, wt, st, bt, bits, group), expected.astype(np.float32),
+                                      err_msg=f"{M}x{N}x{K} g{group}")
+
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 64), (4, 32), (2, 128)])
+def test_prefill_seeded_against_oracle(session, bits, group):
+    """Seeded Affon-generator inputs, bf16 activations: rtol 1e-2 with atol
+    1e-2 * rms(expected) (decoded weights carry bf16 rounding)."""
+    for M, N, K in [(64, 256, 512), (512, 384, 4096), (200, 130, 2048)]:
+        x, packed, s, b = seeded_problem(M, N, K, bits, group, "bf16", "bf16", seed=7)
+        xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+        check_against_oracle(run_mfma(session, xt, wt, st, bt, bits, group), x, packed, s, b, bits, group, True)
+
+
+@pytest.mark.parametrize("shape", [(512, 14336, 4096, 4, 64), (512, 4096, 14336, 4, 64)])
+def test_prefill_full_size_against_exact_kernel(session, shape):
+    """Full prefill shapes: every output element against the reassociated
+    decode kernel (f32 codes, f32 accumulation) on the same device data, and
+    sampled columns of that kernel against the oracle."""
+    M, N, K, bits, group = shape
+    x, packed, s, b = seeded_problem(M, N, K, bits, group, "bf16", "bf16", seed=3)
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    got = run_mfma(session, xt, wt, st, bt, bits, group)
+    exact = session.empty("f32", (M, N))
+    A.quantized_matmul_into(exact, xt, wt, st, bt, bits=bits, group_size=group, implementation="gemv")
+    ref = exact.numpy()
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    assert_close_rtol_atol(got, ref, rtol=1e-2, atol=1e-2 * rms)
+    cols = np.linspace(0, N - 1, 32).astype(int)
+    for c in cols:
+        oracle_col = O.quantized_matmul(x, packed[c:c + 1], s[c:c + 1], b[c:c + 1], bits, group)[:, 0]
+        np.testing.assert_allclose(ref[:, c], oracle_col, rtol=2e-3, atol=1e-4)
+
+
 # ---- quantize / dequantize ----------------------------------------------------------
 
 @pytest.mark.parametrize("bits,group", [(2, 32), (4, 64), (8, 64), (4, 32), (4, 128), (8, 16), (2, 8), (4, 48),
