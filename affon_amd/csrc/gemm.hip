@@ -133,17 +133,92 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
-// Per-wave LDS traffic of one K step.
+// Instruction order of one K step (32 MFMAs, 16 activation-fragment reads,
+// the next step's decode): the decode's LDS reads and the first two chunks'
+// fragment reads go first, then every MFMA is followed by a few decode VALU
+// instructions, so the vector ALU works while the matrix core does.
+template <int kDecodeReads>
+__device__ __forceinline__ void interleave_schedule() {
+  constexpr int kDsRead = 0x100, kMfma = 0x8, kValu = 0x2;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, 8 + kDecodeReads, 0);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 6, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
+  }
+}
+
+// Transfer plan of one wave (64 weight columns) for a weight format.
+//
+// Packed words reach LDS in runs of kColBytes per column: four K steps at a
+// time for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per column), one step at a
+// time for 8-bit (64 bytes) -- so each transfer instruction covers whole
+// half or full 128-byte lines. Inside a column run the 16-byte slots are
+// XOR-swizzled with the column index so the decode's fragment reads are
+// bank-conflict free. Scales and biases come as one 16-byte window per
+// column every four steps (four lanes per column, one dword each; bf16: 8
+// groups, f32: 4 groups), starting at the dword that holds the first group of
+// those 256 k values, which covers all of their groups for the group sizes
+// the kernel accepts; dwords past the row end repeat the row's last dword.
 template <int BITS, typename PT>
-struct StepShape {
-  static constexpr int kWColBytes = 8 * BITS;             // packed bytes of one column per step
-  static constexpr int kWBytes = 64 * kWColBytes;         // this wave's 64 columns
-  static constexpr int kWLoads = kWBytes / 1024;          // 16-byte DMA instructions
-  static constexpr int kPLoads = PT::bytes == 2 ? 2 : 4;  // 4-byte DMA instructions (scales, biases)
-  static constexpr int kPBytes = kPLoads * 256;
-  static constexpr int kALoads = kAGroupsPerWave;         // 16-byte DMA instructions (activations)
-  static constexpr int kOps = kWLoads + kPLoads + kALoads;
-  static_assert(kWBytes % 1024 == 0, "whole DMA instructions");
+struct Plan {
+  static constexpr int kStepsPerW = BITS == 8 ? 1 : 4;           // steps per packed-word transfer
+  static constexpr int kColBytes = 8 * BITS * kStepsPerW;         // bytes per column per transfer
+  static constexpr int kSlots = kColBytes / 16;                   // 16-byte slots per column run
+  static constexpr int kWLoads = 64 * kColBytes / 1024;           // 16-byte DMA instructions per transfer
+  static constexpr int kWBytes = 64 * kColBytes;                  // per wave and buffer
+  static constexpr int kWBufs = kStepsPerW == 1 ? kStages : 2;    // ring depth (buffers)
+  static constexpr int kPLoads = 8;                               // 4-byte DMA: 4 for scales, 4 for biases
+  static constexpr int kPBytes = 2 * 64 * 16;                     // per wave and buffer: 16-byte windows of scales, biases
+  static constexpr int kALoads = kAGroupsPerWave;
+  // LDS read instructions of one step's decode (words, then parameters).
+  static constexpr int kDecodeReads = 2 * (BITS == 8 ? 2 : 1) + 4;
+
+  // Slot (16-byte unit) holding part `part` of column c's run.
+  static __device__ __forceinline__ int slot(int c, int part) {
+    return kSlots == 8 ? part ^ (c & 7) : part ^ ((c >> 1) & 3);
+  }
+
+  // Transfers issued by iteration j (= step index mod 4), in issue order
+  // parameters, words, activations; group 0 = parameters, 1 = words, 2 = activations.
+  static constexpr int group_ops(int j, int g) {
+    return g == 0 ? (j == 0 ? kPLoads : 0) : g == 1 ? (kStepsPerW == 1 || j == 0 ? kWLoads : 0) : kALoads;
+  }
+  static constexpr int ops(int j) { return group_ops(j, 0) + group_ops(j, 1) + group_ops(j, 2); }
+  // Transfers issued after group g of the iteration r iterations before one
+  // with index j, up to the start of that one.
+  static constexpr int ops_after(int j, int r, int g) {
+    const int jr = ((j - r) % 4 + 4) % 4;
+    int n = 0;
+    for (int h = g + 1; h < 3; ++h) n += group_ops(jr, h);
+    for (int i = 1; i < r; ++i) n += ops(((j - i) % 4 + 4) % 4);
+    return n;
+  }
+  // vmcnt bound at the start of iteration j: the activations of its step
+  // (issued three iterations before) and the words and parameters of the
+  // next step (decoded during it) must have landed.
+  static constexpr int wait(int j) {
+    int n = ops_after(j, 3, 2);
+    const int rw = kStepsPerW == 1 ? 3 : (j == 3 ? 3 : j + 4);
+    const int rp = j == 3 ? 3 : j + 4;
+    const int nw = ops_after(j, rw, 1), np = ops_after(j, rp, 0);
+    n = nw < n ? nw : n;
+    n = np < n ? np : n;
+    return n;
+  }
+  static_assert(kWLoads * 1024 == kWBytes, "whole DMA instructions");
 };
 
 // Workgroup tile 128 x 256, K step 64, four waves side by side along N (each
@@ -155,20 +230,19 @@ struct StepShape {
 // chunk c = 4h + kk (k = 8c .. 8c+7). Both operands use this order, so each
 // lane's B operand for a step is one contiguous run of 32 weights.
 //
-// All global reads are direct-to-LDS transfers into a 4-stage ring, issued
-// three steps ahead: per step and wave, four 1 KiB activation transfers
-// (8 rows x 128 bytes each; 16-byte chunk c of row r stored at slot c ^ (r%8)
-// so the A-fragment reads are bank-conflict free), the packed words of the
-// wave's own 64 columns and their scales and biases. A wave decodes B
-// fragments only from its own transfers (no barrier needed for them); the
-// barrier orders the shared activation tile. Step t+1 is decoded while step
-// t's MFMAs run.
+// All global reads are direct-to-LDS transfers: activations into a 4-stage
+// ring three steps ahead (four 1 KiB transfers per wave and step, 8 rows x
+// 128 bytes each; 16-byte chunk c of row r stored at slot c ^ (r%8) so the
+// A-fragment reads are bank-conflict free); packed words, scales and biases
+// of the wave's own 64 columns per Plan. A wave decodes B fragments only from
+// its own transfers (no barrier needed for them); the barrier orders the
+// shared activation tile. Step t+1 is decoded while step t's MFMAs run.
 template <int BITS, typename PT>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
-  using S = StepShape<BITS, PT>;
+  using P = Plan<BITS, PT>;
   __shared__ __attribute__((aligned(16))) uint8_t lds_a[kStages][kAStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_w[kStages][kWaves][S::kWBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_p[kStages][kWaves][S::kPBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_w[P::kWBufs][kWaves][P::kWBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_p[2][kWaves][P::kPBytes];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -190,83 +264,95 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   // Activation transfers: this wave fills 8-row groups kAGroupsPerWave*wave + i.
   // Lane L loads row 8g + L/8, chunk (L%8) ^ (L/8) (rows past M repeat row
   // M-1 and feed only unstored outputs).
-  const uint16_t* a_src[S::kALoads];
+  const uint16_t* a_src[P::kALoads];
 #pragma unroll
-  for (int i = 0; i < S::kALoads; ++i) {
+  for (int i = 0; i < P::kALoads; ++i) {
     const int row = min(m0 + 8 * (kAGroupsPerWave * wave + i) + (lane >> 3), a.M - 1);
     a_src[i] = a.x + static_cast<int64_t>(row) * a.xs0 + 8 * ((lane & 7) ^ (lane >> 3));
   }
-  // Packed-word transfers: 16-byte chunk q = 1024j/16 + L of the wave's slice
-  // is column q / (BITS/2), part q % (BITS/2); the slice is stored in column
-  // order, kWColBytes per column.
-  const uint8_t* w_src[S::kWLoads];
+  // Packed-word transfers: DMA lane L of instruction j writes LDS byte
+  // 1024j + 16L of the wave's buffer = slot (16L % kColBytes) / 16 of local
+  // column (1024j + 16L) / kColBytes, which holds part slot ^ swizzle.
+  const uint8_t* w_src[P::kWLoads];
 #pragma unroll
-  for (int j = 0; j < S::kWLoads; ++j) {
-    const int q = 64 * j + lane;
-    const int col = min(n0 + q / (BITS / 2), a.N - 1);  // columns past N feed unstored outputs
-    w_src[j] = reinterpret_cast<const uint8_t*>(a.w + static_cast<int64_t>(col) * a.ws0) + 16 * (q % (BITS / 2));
+  for (int j = 0; j < P::kWLoads; ++j) {
+    const int pos = 1024 * j + 16 * lane;
+    const int c = pos / P::kColBytes;
+    const int part = P::slot(c, (pos % P::kColBytes) / 16);  // the swizzle is an involution
+    const int col = min(n0 + c, a.N - 1);  // columns past N feed unstored outputs
+    w_src[j] = reinterpret_cast<const uint8_t*>(a.w + static_cast<int64_t>(col) * a.ws0) + 16 * part;
   }
-  // Scale and bias transfers: lane L carries column n0 + L. bf16 parameters
-  // travel as the 4-byte pair holding the step's group(s); f32 parameters as
-  // one 4-byte value per lane half (the groups of k 0..31 and 32..63).
-  const int pcol = min(n0 + lane, a.N - 1);
-  const uint8_t* s_row = a.s + static_cast<int64_t>(pcol) * a.ss0 * PT::bytes;
-  const uint8_t* b_row = a.b + static_cast<int64_t>(pcol) * a.bs0 * PT::bytes;
+  // Parameter windows: DMA lane L of instruction i carries dword L%4 of the
+  // window of local column 16i + L/4, stored at byte 16*(16i + L/4) + 4*(L%4).
+  const int row_dwords = (a.K >> (5 + a.group_shift)) * PT::bytes / 4;  // whole dwords per parameter row
+  const uint8_t* s_col[4];
+  const uint8_t* b_col[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int col = min(n0 + 16 * i + (lane >> 2), a.N - 1);
+    s_col[i] = a.s + static_cast<int64_t>(col) * a.ss0 * PT::bytes;
+    b_col[i] = a.b + static_cast<int64_t>(col) * a.bs0 * PT::bytes;
+  }
+  // First dword of the window for the four steps starting at `step`.
+  auto window = [&](int step) { return (((step * kBK) >> (5 + a.group_shift)) * PT::bytes) >> 2; };
 
-  auto issue = [&](int step, int stage) {
-    const uint32_t wdst = lds_address(lds_w[stage][wave]);
+  auto issue_p = [&](int step) {  // step is a multiple of 4
+    const uint32_t dst = lds_address(lds_p[(step >> 2) & 1][wave]);
+    const int off = 4 * min(window(step) + (lane & 3), row_dwords - 1);
 #pragma unroll
-    for (int j = 0; j < S::kWLoads; ++j) load_lds<16>(w_src[j] + step * S::kWColBytes, wdst + 1024 * j);
-    const uint32_t pdst = lds_address(lds_p[stage][wave]);
-    const int g0 = (step * kBK) >> (5 + a.group_shift);
-    if constexpr (PT::bytes == 2) {
-      load_lds<4>(s_row + 4 * (g0 >> 1), pdst);
-      load_lds<4>(b_row + 4 * (g0 >> 1), pdst + 256);
-    } else {
-      const int g1 = (step * kBK + 32) >> (5 + a.group_shift);
-      load_lds<4>(s_row + 4 * g0, pdst);
-      load_lds<4>(s_row + 4 * g1, pdst + 256);
-      load_lds<4>(b_row + 4 * g0, pdst + 512);
-      load_lds<4>(b_row + 4 * g1, pdst + 768);
-    }
-    const uint32_t adst = lds_address(lds_a[stage]) + 1024 * kAGroupsPerWave * wave;
+    for (int i = 0; i < 4; ++i) load_lds<4>(s_col[i] + off, dst + 256 * i);
 #pragma unroll
-    for (int i = 0; i < S::kALoads; ++i) load_lds<16>(a_src[i] + step * kBK, adst + 1024 * i);
+    for (int i = 0; i < 4; ++i) load_lds<4>(b_col[i] + off, dst + 1024 + 256 * i);
+  };
+  auto issue_w = [&](int step) {  // a transfer's first step
+    const int buf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
+    const uint32_t dst = lds_address(lds_w[buf][wave]);
+    const int64_t off = static_cast<int64_t>(step) * (8 * BITS);
+#pragma unroll
+    for (int j = 0; j < P::kWLoads; ++j) load_lds<16>(w_src[j] + off, dst + 1024 * j);
+  };
+  auto issue_a = [&](int step) {
+    const uint32_t dst = lds_address(lds_a[step & 3]) + 1024 * kAGroupsPerWave * wave;
+#pragma unroll
+    for (int i = 0; i < P::kALoads; ++i) load_lds<16>(a_src[i] + step * kBK, dst + 1024 * i);
   };
 
-  // B fragments of one step for this lane: columns 32*nt + li of the wave's
-  // slice, k 32*lh .. 32*lh+31.
+  // B fragments of one step for this lane: local columns 32*nt + li, k
+  // 32*lh .. 32*lh+31 of the step.
   const float code_scale = BITS == 8 ? 1.0f : 512.0f;
-  auto decode_step = [&](int step, int stage, bf16x8_t (*frag)[4]) {
-    const int g = (step * kBK + 32 * lh) >> (5 + a.group_shift);
+  auto decode_step = [&](int step, bf16x8_t (*frag)[4]) {
+    const int wbuf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
+    const int sub = P::kStepsPerW == 1 ? 0 : (step & 3);  // step within the transfer
+    // Position of this lane's group in the window.
+    const int g = ((step * kBK + 32 * lh) >> (5 + a.group_shift)) - window(step & ~3) * (4 / PT::bytes);
+    const uint8_t* pbuf = lds_p[(step >> 2) & 1][wave];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int c = 32 * nt + li;
-      const uint8_t* wp = lds_w[stage][wave] + c * S::kWColBytes + lh * (S::kWColBytes / 2);
+      const uint8_t* col = lds_w[wbuf][wave] + c * P::kColBytes;
       uint32_t words[BITS];
-      if constexpr (BITS == 2) {
-        const uint2 v = *reinterpret_cast<const uint2*>(wp);
+      if constexpr (BITS == 2) {  // 8 bytes: half of slot `sub`
+        const uint2 v = *reinterpret_cast<const uint2*>(col + 16 * P::slot(c, sub) + 8 * lh);
         words[0] = v.x;
         words[1] = v.y;
       } else {
 #pragma unroll
-        for (int i = 0; i < BITS / 4; ++i) {
-          const u32x4_t v = reinterpret_cast<const u32x4_t*>(wp)[i];
+        for (int i = 0; i < BITS / 4; ++i) {  // 4-bit: part 2*sub + lh; 8-bit: parts 2*lh, 2*lh + 1
+          const int part = BITS == 4 ? 2 * sub + lh : 2 * lh + i;
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(col + 16 * P::slot(c, part));
           words[4 * i] = v.x;
           words[4 * i + 1] = v.y;
           words[4 * i + 2] = v.z;
           words[4 * i + 3] = v.w;
         }
       }
-      const uint32_t* pp = reinterpret_cast<const uint32_t*>(lds_p[stage][wave]);
       float sv, bv;
       if constexpr (PT::bytes == 2) {
-        const int sh = 16 * (1 - (g & 1));  // low half holds the even group
-        sv = __uint_as_float((pp[c] << sh) & 0xffff0000u);
-        bv = __uint_as_float((pp[64 + c] << sh) & 0xffff0000u);
+        sv = __uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(pbuf + 16 * c + 2 * g)) << 16);
+        bv = __uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(pbuf + 1024 + 16 * c + 2 * g)) << 16);
       } else {
-        sv = __uint_as_float(pp[64 * lh + c]);
-        bv = __uint_as_float(pp[128 + 64 * lh + c]);
+        sv = *reinterpret_cast<const float*>(pbuf + 16 * c + 4 * g);
+        bv = *reinterpret_cast<const float*>(pbuf + 1024 + 16 * c + 4 * g);
       }
       decode32<BITS>(words, sv * code_scale, bv, frag[nt]);
     }
@@ -288,32 +374,37 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
       for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
   bf16x8_t bf[2][2][4];
 
-  // Every iteration issues S::kOps transfers per wave, packed words and
-  // parameters first, activations last. Waits (this wave's own transfers):
-  //   step t's activations (issued three iterations before t's):   vmcnt(2*kOps)
-  //   step t+1's words and parameters (first of iteration t-2):   vmcnt(2*kOps + kALoads)
-  issue(0, 0);
-  issue(min(1, last), 1);
-  issue(min(2, last), 2);
-  wait_vmcnt<2 * S::kOps + S::kALoads>();
-  decode_step(0, 0, bf[0]);
+  // Iteration t (j = t % 4) issues, in this order: at j == 0 the parameter
+  // windows and (2/4-bit) the packed words of steps t+4 .. t+7; (8-bit) the
+  // packed words of step t+4; the activations of step t+3. The transfers
+  // before iteration 0 are issued as if by iterations -4 .. -1 (the
+  // activations of "step -1" repeat step 0), so every wait below counts the
+  // same transfers in the prologue as in the loop.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (r == 0) issue_p(0);
+    if (P::kStepsPerW == 1 || r == 0) issue_w(min(r, last));
+    issue_a(min(max(r - 1, 0), last));
+  }
+  wait_vmcnt<P::ops_after(0, 4, 1)>();  // words (issued after the parameters) of step 0
+  decode_step(0, bf[0]);
 
 #define AFFON_QGEMM_STEP(J)                                                                                   \
   {                                                                                                           \
     constexpr int RB = (J)&1;                                                                                 \
-    wait_vmcnt<2 * S::kOps>();                                                                                \
+    wait_vmcnt<P::wait(J)>();                                                                                 \
     __syncthreads();                                                                                          \
-    issue(min(t + 3, last), ((J) + 3) & 3);                                                                   \
+    if ((J) == 0) issue_p(min(t + 4, last & ~3));                                                            \
+    if (P::kStepsPerW == 1 || (J) == 0) issue_w(min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)));        \
+    issue_a(min(t + 3, last));                                                                                \
     _Pragma("unroll") for (int kk = 0; kk < 4; ++kk) {                                                        \
       bf16x8_t af[4];                                                                                         \
       _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) af[mt] = read_a(J, mt, kk);                            \
       _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) _Pragma("unroll") for (int nt = 0; nt < 2; ++nt)       \
           acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[RB][nt][kk], acc[mt][nt], 0, 0, 0); \
-      if (kk == 1) {                                                                                          \
-        wait_vmcnt<2 * S::kOps + S::kALoads>();                                                               \
-        decode_step(min(t + 1, last), ((J) + 1) & 3, bf[RB ^ 1]);                                             \
-      }                                                                                                       \
+      if (kk == 1) decode_step(min(t + 1, last), bf[RB ^ 1]);                                                 \
     }                                                                                                         \
+    interleave_schedule<P::kDecodeReads>();                                                                   \
     ++t;                                                                                                      \
   }
 
@@ -361,9 +452,13 @@ bool mfma_supports(const QmmProblem& p) {
   if ((gq & (gq - 1)) != 0) return false;  // group index by shift
   if (reinterpret_cast<uintptr_t>(p.x) % 16 != 0 || (p.xs0 * 2) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0 || p.ws0 % 4 != 0) return false;
-  // Parameters travel in 4-byte units: bf16 pairs must not straddle a row end.
+  // Parameters travel in dwords (rows of whole dwords, dword-aligned) and a
+  // 16-byte window must hold every group of four K steps (f32: groups of 64
+  // or more).
+  const int64_t pbytes = p.p_dtype == AFFON_ROCM_BF16 ? 2 : 4;
   if (reinterpret_cast<uintptr_t>(p.s) % 4 != 0 || reinterpret_cast<uintptr_t>(p.b) % 4 != 0) return false;
-  if (p.p_dtype == AFFON_ROCM_BF16 && (p.ss0 % 2 != 0 || p.bs0 % 2 != 0 || (p.K / p.group) % 2 != 0)) return false;
+  if ((p.ss0 * pbytes) % 4 != 0 || (p.bs0 * pbytes) % 4 != 0 || (p.K / p.group * pbytes) % 4 != 0) return false;
+  if (4 * kBK / p.group > 16 / pbytes) return false;
   if (p.M > (int64_t(1) << 30) || p.N > (int64_t(1) << 30) || p.K > (int64_t(1) << 30)) return false;
   if (((p.N + kBN - 1) / kBN) * ((p.M + kBM - 1) / kBM) > (int64_t(1) << 31) - 1) return false;
   return true;

@@ -356,7 +356,8 @@ def test_prefill_exact_integer_products(session, bits, p_dtype, rng):
     """Power-of-two scales and zero biases keep every decoded weight exact in
     bf16 and every partial sum exact in f32: the GEMM must match exactly,
     including partial M/N tiles and one or many K steps."""
-    for M, N, K, group in [(64, 128, 256, 32), (100, 40, 512, 64), (300, 300, 1024, 128), (515, 129, 4096, 64)]:
+    for M, N, K, group in [(64, 128, 256, 32), (100, 40, 512, 64), (300, 300, 1024, 128), (515, 129, 4096, 64),
+                           (256, 256, 11008, 128)]:
         q = rng.integers(0, 1 << bits, size=(N, K))
         x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
         s = 2.0 ** rng.integers(-3, 1, size=(N, K // group))
@@ -365,6 +366,15 @@ def test_prefill_exact_integer_products(session, bits, p_dtype, rng):
         xt = upload(session, storage(x, "bf16"), "bf16")
         wt = upload(session, pack_codes(q, bits), "u32")
         st, bt = upload(session, storage(s, p_dtype), p_dtype), upload(session, storage(b, p_dtype), p_dtype)
+        if p_dtype == "f32" and group == 32:
+            # f32 groups of 32 do not fit the kernel's parameter window: it
+            # declines, and AUTO falls back to a path that is still exact here.
+            with pytest.raises(_native.NativeError, match="cannot run this shape"):
+                run_mfma(session, xt, wt, st, bt, bits, group)
+            out = session.empty("f32", (M, N))
+            A.quantized_matmul_into(out, xt, wt, st, bt, bits=bits, group_size=group, policy="approximate")
+            np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32))
+            continue
         np.testing.assert_array_equal(run_mfma(session, xt, wt, st, bt, bits, group), expected.astype(np.float32),
                                       err_msg=f"{M}x{N}x{K} g{group}")
 
