@@ -14,6 +14,8 @@
 // MFMA B fragments in registers (codes -> f32 via FP8 conversion for 2/4-bit
 // or v_cvt_f32_ubyte for 8-bit -> s*q + b -> bf16).
 
+#include <type_traits>
+
 #include "device.h"
 #include "internal.h"
 
@@ -133,30 +135,91 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
-// Instruction order of one K step (32 MFMAs, 16 activation-fragment reads,
-// the next step's decode): the decode's LDS reads and the first two chunks'
-// fragment reads go first, then every MFMA is followed by a few decode VALU
-// instructions, so the vector ALU works while the matrix core does.
-template <int kDecodeReads>
-__device__ __forceinline__ void interleave_schedule() {
-  constexpr int kDsRead = 0x100, kMfma = 0x8, kValu = 0x2;
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 8 + kDecodeReads, 0);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 6, 0);
+// Compile-time unrolled loop: f(std::integral_constant<int, I>) for I in [I0, N).
+template <int I, int N>
+struct Unroll {
+  template <class F>
+  __device__ __forceinline__ static void run(F&& f) {
+    f(std::integral_constant<int, I>{});
+    Unroll<I + 1, N>::run(f);
   }
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
+};
+template <int N>
+struct Unroll<N, N> {
+  template <class F>
+  __device__ __forceinline__ static void run(F&&) {}
+};
+
+// Inputs of one step's decode for one lane: BITS packed words (32 weights)
+// and the raw parameter bits of each of the lane's two columns.
+template <int BITS>
+struct DecodeIn {
+  uint32_t words[2][BITS];
+  uint32_t s_raw[2], b_raw[2];
+};
+
+// Intermediate values of the decode while its pieces are spread over a
+// step's MFMAs.
+struct DecodeTmp {
+  float s[2], b[2];
+  f32x2_t lo[4], hi[4];
+};
+
+template <typename PT>
+__device__ __forceinline__ float widen_param(uint32_t raw) {
+  return PT::bytes == 2 ? __uint_as_float(raw << 16) : __uint_as_float(raw);
+}
+
+// Piece p (0..31) of a step's decode: the 64 weights of a lane (2 columns x
+// 32 k) split into 32 pieces of 5-6 VALU instructions, one per MFMA. Words
+// are decoded in order; a word takes 16/BITS pieces: for 2/4-bit first one
+// piece per code mask (FP8 conversion of the masked bytes: codes n < 16 read
+// as n * 2^-9, the scale carries the 2^9), then pieces that apply s*q + b and
+// pack bf16 pairs; for 8-bit two pieces of two bytes each. Pair q of column
+// nt (weights 2q, 2q+1 of the lane's run) goes to out[nt][q/4][q%4].
+template <int BITS, typename PT, int p>
+__device__ __forceinline__ void decode_piece(const DecodeIn<BITS>& in, DecodeTmp& d, u32x4_t (&out)[2][4],
+                                             float code_scale) {
+  constexpr int kPieces = 16 / BITS;  // pieces per word
+  constexpr int wi = p / kPieces, st = p % kPieces;
+  constexpr int nt = wi / BITS, w = wi % BITS;
+  if constexpr (st == 0 && w == 0) {
+    d.s[nt] = widen_param<PT>(in.s_raw[nt]) * code_scale;
+    d.b[nt] = widen_param<PT>(in.b_raw[nt]);
   }
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
+  const float s = d.s[nt], b = d.b[nt];
+  const uint32_t word = in.words[nt][w];
+  if constexpr (BITS == 4) {  // code 2j + t sits in byte j of mask t
+    if constexpr (st < 2) {
+      const uint32_t m = (word >> (4 * st)) & 0x0f0f0f0fu;
+      d.lo[st] = __builtin_amdgcn_cvt_pk_f32_fp8(m, false);
+      d.hi[st] = __builtin_amdgcn_cvt_pk_f32_fp8(m, true);
+    } else {
+      const f32x2_t* v = st == 2 ? d.lo : d.hi;  // codes 0..3 or 4..7
+      constexpr int q = 4 * w + 2 * (st - 2);
+      out[nt][q / 4][q % 4] = pack_bf16(fmaf(v[0].x, s, b), fmaf(v[1].x, s, b));
+      out[nt][(q + 1) / 4][(q + 1) % 4] = pack_bf16(fmaf(v[0].y, s, b), fmaf(v[1].y, s, b));
+    }
+  } else if constexpr (BITS == 2) {  // code 4j + t sits in byte j of mask t
+    if constexpr (st < 4) {
+      const uint32_t m = (word >> (2 * st)) & 0x03030303u;
+      d.lo[st] = __builtin_amdgcn_cvt_pk_f32_fp8(m, false);
+      d.hi[st] = __builtin_amdgcn_cvt_pk_f32_fp8(m, true);
+    } else {
+      constexpr int j = st - 4;  // codes 4j .. 4j+3
+      float v[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
+      for (int t = 0; t < 4; ++t) v[t] = j == 0 ? d.lo[t].x : j == 1 ? d.lo[t].y : j == 2 ? d.hi[t].x : d.hi[t].y;
+      constexpr int q = 8 * w + 2 * j;
+      out[nt][q / 4][q % 4] = pack_bf16(fmaf(v[0], s, b), fmaf(v[1], s, b));
+      out[nt][(q + 1) / 4][(q + 1) % 4] = pack_bf16(fmaf(v[2], s, b), fmaf(v[3], s, b));
+    }
+  } else {  // bytes 2*st and 2*st+1 of the word
+    const uint32_t v = opaque(word);
+    const float q0 = static_cast<float>((v >> (16 * st)) & 0xffu);
+    const float q1 = static_cast<float>((v >> (16 * st + 8)) & 0xffu);
+    constexpr int q = 2 * w + st;
+    out[nt][q / 4][q % 4] = pack_bf16(fmaf(q0, s, b), fmaf(q1, s, b));
   }
 }
 
@@ -183,8 +246,6 @@ struct Plan {
   static constexpr int kPLoads = 8;                               // 4-byte DMA: 4 for scales, 4 for biases
   static constexpr int kPBytes = 2 * 64 * 16;                     // per wave and buffer: 16-byte windows of scales, biases
   static constexpr int kALoads = kAGroupsPerWave;
-  // LDS read instructions of one step's decode (words, then parameters).
-  static constexpr int kDecodeReads = 2 * (BITS == 8 ? 2 : 1) + 4;
 
   // Slot (16-byte unit) holding part `part` of column c's run.
   static __device__ __forceinline__ int slot(int c, int part) {
@@ -317,44 +378,41 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
     for (int i = 0; i < P::kALoads; ++i) load_lds<16>(a_src[i] + step * kBK, dst + 1024 * i);
   };
 
-  // B fragments of one step for this lane: local columns 32*nt + li, k
+  // Decode inputs of one step for this lane: local columns 32*nt + li, k
   // 32*lh .. 32*lh+31 of the step.
   const float code_scale = BITS == 8 ? 1.0f : 512.0f;
-  auto decode_step = [&](int step, bf16x8_t (*frag)[4]) {
+  auto load_decode = [&](int step, DecodeIn<BITS>& in) {
     const int wbuf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
     const int sub = P::kStepsPerW == 1 ? 0 : (step & 3);  // step within the transfer
-    // Position of this lane's group in the window.
+    // Position of this lane's group in the parameter window.
     const int g = ((step * kBK + 32 * lh) >> (5 + a.group_shift)) - window(step & ~3) * (4 / PT::bytes);
     const uint8_t* pbuf = lds_p[(step >> 2) & 1][wave];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int c = 32 * nt + li;
       const uint8_t* col = lds_w[wbuf][wave] + c * P::kColBytes;
-      uint32_t words[BITS];
       if constexpr (BITS == 2) {  // 8 bytes: half of slot `sub`
         const uint2 v = *reinterpret_cast<const uint2*>(col + 16 * P::slot(c, sub) + 8 * lh);
-        words[0] = v.x;
-        words[1] = v.y;
+        in.words[nt][0] = v.x;
+        in.words[nt][1] = v.y;
       } else {
 #pragma unroll
         for (int i = 0; i < BITS / 4; ++i) {  // 4-bit: part 2*sub + lh; 8-bit: parts 2*lh, 2*lh + 1
           const int part = BITS == 4 ? 2 * sub + lh : 2 * lh + i;
           const u32x4_t v = *reinterpret_cast<const u32x4_t*>(col + 16 * P::slot(c, part));
-          words[4 * i] = v.x;
-          words[4 * i + 1] = v.y;
-          words[4 * i + 2] = v.z;
-          words[4 * i + 3] = v.w;
+          in.words[nt][4 * i] = v.x;
+          in.words[nt][4 * i + 1] = v.y;
+          in.words[nt][4 * i + 2] = v.z;
+          in.words[nt][4 * i + 3] = v.w;
         }
       }
-      float sv, bv;
       if constexpr (PT::bytes == 2) {
-        sv = __uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(pbuf + 16 * c + 2 * g)) << 16);
-        bv = __uint_as_float(static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(pbuf + 1024 + 16 * c + 2 * g)) << 16);
+        in.s_raw[nt] = *reinterpret_cast<const uint16_t*>(pbuf + 16 * c + 2 * g);
+        in.b_raw[nt] = *reinterpret_cast<const uint16_t*>(pbuf + 1024 + 16 * c + 2 * g);
       } else {
-        sv = *reinterpret_cast<const float*>(pbuf + 16 * c + 4 * g);
-        bv = *reinterpret_cast<const float*>(pbuf + 1024 + 16 * c + 4 * g);
+        in.s_raw[nt] = *reinterpret_cast<const uint32_t*>(pbuf + 16 * c + 4 * g);
+        in.b_raw[nt] = *reinterpret_cast<const uint32_t*>(pbuf + 1024 + 16 * c + 4 * g);
       }
-      decode32<BITS>(words, sv * code_scale, bv, frag[nt]);
     }
   };
 
@@ -372,7 +430,8 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mt][nt][v] = 0.0f;
-  bf16x8_t bf[2][2][4];
+  u32x4_t bf[2][2][4];  // B fragments (bf16 pairs) of two steps: [step parity][nt][kk]
+  DecodeTmp dtmp;
 
   // Iteration t (j = t % 4) issues, in this order: at j == 0 the parameter
   // windows and (2/4-bit) the packed words of steps t+4 .. t+7; (8-bit) the
@@ -387,25 +446,42 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
     issue_a(min(max(r - 1, 0), last));
   }
   wait_vmcnt<P::ops_after(0, 4, 1)>();  // words (issued after the parameters) of step 0
-  decode_step(0, bf[0]);
+  {
+    DecodeIn<BITS> din;
+    load_decode(0, din);
+    Unroll<0, 32>::run([&](auto ic) { decode_piece<BITS, PT, decltype(ic)::value>(din, dtmp, bf[0], code_scale); });
+  }
 
-#define AFFON_QGEMM_STEP(J)                                                                                   \
-  {                                                                                                           \
-    constexpr int RB = (J)&1;                                                                                 \
-    wait_vmcnt<P::wait(J)>();                                                                                 \
-    __syncthreads();                                                                                          \
-    if ((J) == 0) issue_p(min(t + 4, last & ~3));                                                            \
-    if (P::kStepsPerW == 1 || (J) == 0) issue_w(min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)));        \
-    issue_a(min(t + 3, last));                                                                                \
-    _Pragma("unroll") for (int kk = 0; kk < 4; ++kk) {                                                        \
-      bf16x8_t af[4];                                                                                         \
-      _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) af[mt] = read_a(J, mt, kk);                            \
-      _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) _Pragma("unroll") for (int nt = 0; nt < 2; ++nt)       \
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[RB][nt][kk], acc[mt][nt], 0, 0, 0); \
-      if (kk == 1) decode_step(min(t + 1, last), bf[RB ^ 1]);                                                 \
-    }                                                                                                         \
-    interleave_schedule<P::kDecodeReads>();                                                                   \
-    ++t;                                                                                                      \
+  // One K step, hand-ordered: decode inputs of step t+1 and the activation
+  // fragments of chunks 0 and 1 are read first, then the transfers are
+  // issued, then each of the 32 MFMAs is followed by one decode piece (the
+  // scheduling barriers keep this order, so the vector ALU works while the
+  // matrix core does); chunk kk+1's fragments are read when chunk kk starts.
+#define AFFON_QGEMM_STEP(J)                                                                                     \
+  {                                                                                                             \
+    constexpr int RB = (J)&1;                                                                                   \
+    wait_vmcnt<P::wait(J)>();                                                                                   \
+    __syncthreads();                                                                                            \
+    DecodeIn<BITS> din;                                                                                         \
+    load_decode(min(t + 1, last), din);                                                                         \
+    bf16x8_t af[2][4];                                                                                          \
+    _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) af[0][mt] = read_a(J, mt, 0);                              \
+    _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) af[1][mt] = read_a(J, mt, 1);                              \
+    if ((J) == 0) issue_p(min(t + 4, last & ~3));                                                              \
+    if (P::kStepsPerW == 1 || (J) == 0) issue_w(min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)));          \
+    issue_a(min(t + 3, last));                                                                                  \
+    Unroll<0, 32>::run([&](auto ic) {                                                                           \
+      constexpr int p = decltype(ic)::value;                                                                    \
+      constexpr int kk = p / 8, mt = (p % 8) / 2, nt = p % 2;                                                   \
+      if constexpr (p % 8 == 0 && kk >= 1 && kk < 3) {                                                          \
+        _Pragma("unroll") for (int m = 0; m < 4; ++m) af[(kk + 1) & 1][m] = read_a(J, m, kk + 1);              \
+      }                                                                                                         \
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][mt], __builtin_bit_cast(bf16x8_t, bf[RB][nt][kk]), \
+                                                            acc[mt][nt], 0, 0, 0);                              \
+      decode_piece<BITS, PT, p>(din, dtmp, bf[RB ^ 1], code_scale);                                            \
+      __builtin_amdgcn_sched_barrier(0);                                                                        \
+    });                                                                                                         \
+    ++t;                                                                                                        \
   }
 
   for (int t = 0; t < steps;) {
