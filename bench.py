@@ -160,7 +160,9 @@ class Workload:
 def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0) -> dict:
     """The oracle (the restated scalar CPU kernel) timed on this host, single
     threaded as the reference's CPU kernel is (AFFON_CPU_THREADS=1), over a
-    bounded sample of output rows; also checks those rows against the GPU."""
+    bounded sample of about `seconds` of CPU work: a prefix of output rows
+    when the whole workload takes longer, else repeated whole passes. Also
+    checks the rows it computed against the GPU output."""
     from oracle import oracle as O
     x, packed, scales, biases = work.host_operands()
     M, N, K = work.M, work.N, work.K
@@ -169,12 +171,14 @@ def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0) -> 
     O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, probe))
     per_row = (time.perf_counter() - t0) / probe
     rows = int(min(N, max(probe, seconds / max(per_row, 1e-9))))
+    passes = max(1, int(seconds / max(per_row * N, 1e-9))) if rows == N else 1
     t0 = time.perf_counter()
-    ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, rows))
+    for _ in range(passes):
+        ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, rows))
     elapsed = time.perf_counter() - t0
     xbytes = 2 if work.x_dtype == "bf16" else 4
     pbytes = 2 if work.p_dtype == "bf16" else 4
-    sample_bytes = algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
+    sample_bytes = passes * algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
     err = float(np.abs(gpu_out[:, :rows].astype(np.float64) - ref[:, :rows]).max())
     cpu = platform.processor() or platform.machine()
     try:
@@ -183,8 +187,9 @@ def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0) -> 
     except (OSError, StopIteration):
         pass
     return {"value": round(sample_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle scalar quantized_matmul, rows 0..{rows} of {N} ({rows / N:.1%}) of the timed "
-                      f"workload, {elapsed:.1f} s on 1 thread; host {cpu}, nproc {os.cpu_count()}",
+            "sample": (f"oracle scalar quantized_matmul over the timed workload, "
+                       + (f"{passes} whole passes" if rows == N else f"rows 0..{rows} of {N} ({rows / N:.1%})")
+                       + f", {elapsed:.1f} s on 1 thread; host {cpu}, nproc {os.cpu_count()}"),
             "max_abs_err_vs_gpu": err}
 
 
@@ -195,10 +200,29 @@ def roofline_gemv(work: Workload, ms: float, traffic) -> dict:
 
 
 def load_traffic(name: str):
+    """HBM bytes per launch of the workload's kernel: FETCH_SIZE + WRITE_SIZE
+    from counter runs, each scaled by the same counter's reading for a copy of
+    known size (profiles/traffic.json, written from those runs)."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
-    return json.loads(path.read_text()).get(name)
+    entry = json.loads(path.read_text()).get(name)
+    return None if entry is None else entry["traffic_bytes"]
+
+
+def copy_calibration(session) -> int:
+    """Copies of a known size, profiled with the same byte counters as the
+    kernels, give the factor from counter units to bytes."""
+    from affon_amd import _native
+    lib = _native.load()
+    nbytes = 256 << 20
+    src, dst = session.empty("u32", (nbytes // 4,)), session.empty("u32", (nbytes // 4,))
+    for _ in range(8):
+        _native.check(lib.affon_rocm_memcpy_d2d(session._handle, dst.data_ptr, src.data_ptr, nbytes), "copy")
+    session.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 8}), flush=True)
+    session.dispose()
+    return 0
 
 
 def main() -> int:
@@ -208,7 +232,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--launch", choices=["graph", "stream"], default="graph")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
-    parser.add_argument("--only", default="", help="comma-separated subset of extra workloads to run")
+    parser.add_argument("--only", default="", help="comma-separated subset of extra workloads to run ('none': no extras)")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run 8 device-to-device copies of 256 MiB (for scaling hardware byte counters)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the quantized linear path has no multi-GPU execution "
@@ -219,6 +245,8 @@ def main() -> int:
     hip = Hip()
     session = A.Session("rocm")
     use_graph = args.launch == "graph"
+    if args.copy_calibration:
+        return copy_calibration(session)
 
     main_work = Workload(session, "decode_8bit_g64_m1", 1, 14336, 4096, 8, 64)
     ms = main_work.time(hip, args.steps, args.warmup, use_graph)
@@ -227,7 +255,7 @@ def main() -> int:
     roofline = roofline_gemv(main_work, ms, load_traffic(main_work.name))
     impl = main_work.implementation
     sets = main_work.sets
-    baseline = cpu_baseline(main_work, gpu_out, args.cpu_seconds)
+    baseline = cpu_baseline(main_work, gpu_out, args.cpu_seconds) if args.cpu_seconds > 0 else None
     main_work.release()
 
     extras = {}
