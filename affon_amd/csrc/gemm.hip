@@ -229,8 +229,9 @@ __device__ __forceinline__ void decode_piece(const DecodeIn<BITS>& in, DecodeTmp
 // time for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per column), one step at a
 // time for 8-bit (64 bytes) -- so each transfer instruction covers whole
 // half or full 128-byte lines. Inside a column run the 16-byte slots are
-// XOR-swizzled with the column index so the decode's fragment reads are
-// bank-conflict free. Scales and biases come as one 16-byte window per
+// XOR-swizzled with the column index so that the decode's fragment reads
+// (lanes = consecutive columns) are bank-conflict free whether the LDS serves
+// 8 lanes x 16 bytes (128 bytes) or 16 lanes x 16 bytes (256 bytes) per cycle. Scales and biases come as one 16-byte window per
 // column every four steps (four lanes per column, one dword each; bf16: 8
 // groups, f32: 4 groups), starting at the dword that holds the first group of
 // those 256 k values, which covers all of their groups for the group sizes
@@ -247,9 +248,13 @@ struct Plan {
   static constexpr int kPBytes = 2 * 64 * 16;                     // per wave and buffer: 16-byte windows of scales, biases
   static constexpr int kALoads = kAGroupsPerWave;
 
-  // Slot (16-byte unit) holding part `part` of column c's run.
+  // Slot (16-byte unit) holding part `part` of column c's run. 128-byte runs:
+  // within 8 consecutive columns the slots differ; columns c and c+8 (same
+  // 128-byte bank phase in a 256-byte window) differ in slot bit 0. 64-byte
+  // runs: even columns 0,2,4,6 (and odd 1,3,5,7) use different slots, and so
+  // do columns c, c+4, c+8, c+12.
   static __device__ __forceinline__ int slot(int c, int part) {
-    return kSlots == 8 ? part ^ (c & 7) : part ^ ((c >> 1) & 3);
+    return kSlots == 8 ? part ^ (c & 7) ^ ((c >> 3) & 1) : part ^ (((c >> 1) ^ (c >> 3)) & 3);
   }
 
   // Transfers issued by iteration j (= step index mod 4), in issue order
@@ -293,8 +298,9 @@ struct Plan {
 //
 // All global reads are direct-to-LDS transfers: activations into a 4-stage
 // ring three steps ahead (four 1 KiB transfers per wave and step, 8 rows x
-// 128 bytes each; 16-byte chunk c of row r stored at slot c ^ (r%8) so the
-// A-fragment reads are bank-conflict free); packed words, scales and biases
+// 128 bytes each; 16-byte chunk c of row r stored at slot
+// c ^ (r%8) ^ ((r/8)%2), so the A-fragment reads -- consecutive rows, one
+// chunk -- are bank-conflict free for 8- and 16-lane LDS phases); packed words, scales and biases
 // of the wave's own 64 columns per Plan. A wave decodes B fragments only from
 // its own transfers (no barrier needed for them); the barrier orders the
 // shared activation tile. Step t+1 is decoded while step t's MFMAs run.
@@ -322,14 +328,16 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   const int steps = a.K / kBK;
   const int last = steps - 1;
 
-  // Activation transfers: this wave fills 8-row groups kAGroupsPerWave*wave + i.
-  // Lane L loads row 8g + L/8, chunk (L%8) ^ (L/8) (rows past M repeat row
-  // M-1 and feed only unstored outputs).
+  // Activation transfers: this wave fills 8-row groups g = kAGroupsPerWave*wave + i.
+  // Lane L writes slot L%8 of local row 8g + L/8, so it loads chunk
+  // (L%8) ^ (L/8) ^ (g%2) (rows past M repeat row M-1 and feed only unstored
+  // outputs).
+  static_assert(kAGroupsPerWave % 2 == 0, "group parity is i % 2");
   const uint16_t* a_src[P::kALoads];
 #pragma unroll
   for (int i = 0; i < P::kALoads; ++i) {
     const int row = min(m0 + 8 * (kAGroupsPerWave * wave + i) + (lane >> 3), a.M - 1);
-    a_src[i] = a.x + static_cast<int64_t>(row) * a.xs0 + 8 * ((lane & 7) ^ (lane >> 3));
+    a_src[i] = a.x + static_cast<int64_t>(row) * a.xs0 + 8 * ((lane & 7) ^ (lane >> 3) ^ (i & 1));
   }
   // Packed-word transfers: DMA lane L of instruction j writes LDS byte
   // 1024j + 16L of the wave's buffer = slot (16L % kColBytes) / 16 of local
@@ -357,25 +365,28 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   // First dword of the window for the four steps starting at `step`.
   auto window = [&](int step) { return (((step * kBK) >> (5 + a.group_shift)) * PT::bytes) >> 2; };
 
-  auto issue_p = [&](int step) {  // step is a multiple of 4
-    const uint32_t dst = lds_address(lds_p[(step >> 2) & 1][wave]);
+  // Single transfer instructions: parameter window i (0..3 scales, 4..7
+  // biases) of the four steps starting at `step` (a multiple of 4); packed-word
+  // instruction j of the transfer starting at `step`; activation group i of `step`.
+  auto issue_p = [&](int step, int i) {
+    const uint32_t dst = lds_address(lds_p[(step >> 2) & 1][wave]) + (i < 4 ? 256 * i : 1024 + 256 * (i - 4));
     const int off = 4 * min(window(step) + (lane & 3), row_dwords - 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) load_lds<4>(s_col[i] + off, dst + 256 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) load_lds<4>(b_col[i] + off, dst + 1024 + 256 * i);
+    load_lds<4>((i < 4 ? s_col[i] : b_col[i - 4]) + off, dst);
   };
-  auto issue_w = [&](int step) {  // a transfer's first step
+  auto issue_w = [&](int step, int j) {
     const int buf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
-    const uint32_t dst = lds_address(lds_w[buf][wave]);
-    const int64_t off = static_cast<int64_t>(step) * (8 * BITS);
-#pragma unroll
-    for (int j = 0; j < P::kWLoads; ++j) load_lds<16>(w_src[j] + off, dst + 1024 * j);
+    load_lds<16>(w_src[j] + static_cast<int64_t>(step) * (8 * BITS), lds_address(lds_w[buf][wave]) + 1024 * j);
   };
-  auto issue_a = [&](int step) {
-    const uint32_t dst = lds_address(lds_a[step & 3]) + 1024 * kAGroupsPerWave * wave;
-#pragma unroll
-    for (int i = 0; i < P::kALoads; ++i) load_lds<16>(a_src[i] + step * kBK, dst + 1024 * i);
+  auto issue_a = [&](int step, int i) {
+    load_lds<16>(a_src[i] + step * kBK, lds_address(lds_a[step & 3]) + 1024 * (kAGroupsPerWave * wave + i));
+  };
+  // All transfers of the iteration with index j, in the order the waits count them.
+  auto issue_all = [&](int j, int pstep, int wstep, int astep) {
+    if (j == 0)
+      for (int i = 0; i < P::kPLoads; ++i) issue_p(pstep, i);
+    if (P::kStepsPerW == 1 || j == 0)
+      for (int i = 0; i < P::kWLoads; ++i) issue_w(wstep, i);
+    for (int i = 0; i < P::kALoads; ++i) issue_a(astep, i);
   };
 
   // Decode inputs of one step for this lane: local columns 32*nt + li, k
@@ -419,7 +430,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   // A fragment (mt, kk) of this lane: row 32*mt + li, chunk 4*lh + kk.
   auto read_a = [&](int stage, int mt, int kk) -> bf16x8_t {
     const int row = 32 * mt + li;
-    const int slot = (4 * lh + kk) ^ (row & 7);
+    const int slot = (4 * lh + kk) ^ (row & 7) ^ ((row >> 3) & 1);
     return *reinterpret_cast<const bf16x8_t*>(&lds_a[stage][(row >> 3) * 1024 + (8 * (row & 7) + slot) * 16]);
   };
 
@@ -440,11 +451,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   // activations of "step -1" repeat step 0), so every wait below counts the
   // same transfers in the prologue as in the loop.
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (r == 0) issue_p(0);
-    if (P::kStepsPerW == 1 || r == 0) issue_w(min(r, last));
-    issue_a(min(max(r - 1, 0), last));
-  }
+  for (int r = 0; r < 4; ++r) issue_all(r, 0, min(r, last), min(max(r - 1, 0), last));
   wait_vmcnt<P::ops_after(0, 4, 1)>();  // words (issued after the parameters) of step 0
   {
     DecodeIn<BITS> din;
@@ -453,10 +460,11 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   }
 
   // One K step, hand-ordered: decode inputs of step t+1 and the activation
-  // fragments of chunks 0 and 1 are read first, then the transfers are
-  // issued, then each of the 32 MFMAs is followed by one decode piece (the
-  // scheduling barriers keep this order, so the vector ALU works while the
-  // matrix core does); chunk kk+1's fragments are read when chunk kk starts.
+  // fragments of chunks 0 and 1 are read first; then each of the 32 MFMAs is
+  // followed by one decode piece and, spread evenly, the iteration's transfer
+  // instructions (the scheduling barriers keep this order, so the vector ALU
+  // and the memory pipeline work while the matrix core does); chunk kk+1's
+  // fragments are read when chunk kk starts.
 #define AFFON_QGEMM_STEP(J)                                                                                     \
   {                                                                                                             \
     constexpr int RB = (J)&1;                                                                                   \
@@ -467,9 +475,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
     bf16x8_t af[2][4];                                                                                          \
     _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) af[0][mt] = read_a(J, mt, 0);                              \
     _Pragma("unroll") for (int mt = 0; mt < 4; ++mt) af[1][mt] = read_a(J, mt, 1);                              \
-    if ((J) == 0) issue_p(min(t + 4, last & ~3));                                                              \
-    if (P::kStepsPerW == 1 || (J) == 0) issue_w(min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)));          \
-    issue_a(min(t + 3, last));                                                                                  \
+    const int pstep = min(t + 4, last & ~3);                                                                    \
+    const int wstep = min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3));                                      \
+    const int astep = min(t + 3, last);                                                                         \
     Unroll<0, 32>::run([&](auto ic) {                                                                           \
       constexpr int p = decltype(ic)::value;                                                                    \
       constexpr int kk = p / 8, mt = (p % 8) / 2, nt = p % 2;                                                   \
@@ -479,6 +487,15 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
       acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][mt], __builtin_bit_cast(bf16x8_t, bf[RB][nt][kk]), \
                                                             acc[mt][nt], 0, 0, 0);                              \
       decode_piece<BITS, PT, p>(din, dtmp, bf[RB ^ 1], code_scale);                                            \
+      constexpr int nP = P::group_ops(J, 0), nW = P::group_ops(J, 1), nX = nP + nW + P::group_ops(J, 2);        \
+      Unroll<0, nX>::run([&](auto kc) {                                                                         \
+        constexpr int k = decltype(kc)::value;                                                                  \
+        if constexpr (k * 32 / nX == p) {                                                                       \
+          if constexpr (k < nP) issue_p(pstep, k);                                                              \
+          else if constexpr (k < nP + nW) issue_w(wstep, k - nP);                                               \
+          else issue_a(astep, k - nP - nW);                                                                     \
+        }                                                                                                       \
+      });                                                                                                       \
       __builtin_amdgcn_sched_barrier(0);                                                                        \
     });                                                                                                         \
     ++t;                                                                                                        \
