@@ -21,7 +21,41 @@
 struct affon_rocm_session {
   int device = 0;
   hipStream_t stream = nullptr;
+  affon::Workspace* workspace = nullptr;
 };
+
+namespace affon {
+
+Workspace::~Workspace() {
+  if (ptr_ != nullptr && hipSetDevice(device_) == hipSuccess) (void)hipFree(ptr_);
+}
+
+void* Workspace::get(size_t bytes) {
+  if (bytes <= bytes_) return ptr_;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream_, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) return nullptr;
+  // Work already enqueued may still use the old memory.
+  if (hipStreamSynchronize(stream_) != hipSuccess) return nullptr;
+  if (ptr_ != nullptr) (void)hipFree(ptr_);
+  ptr_ = nullptr;
+  bytes_ = 0;
+  const size_t rounded = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+  if (hipMalloc(&ptr_, rounded) != hipSuccess) {
+    ptr_ = nullptr;
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (hipMemset(ptr_, 0, rounded) != hipSuccess) {
+    (void)hipFree(ptr_);
+    ptr_ = nullptr;
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  bytes_ = rounded;
+  return ptr_;
+}
+
+}  // namespace affon
 
 namespace {
 
@@ -154,7 +188,7 @@ struct Candidate {
   // 2 approximate (rounds decoded weights to bf16).
   int numerical_class;
   bool (*supports)(const affon::QmmProblem&);
-  hipError_t (*launch)(const affon::QmmProblem&, hipStream_t);
+  hipError_t (*launch)(const affon::QmmProblem&, const affon::Launch&);
 };
 
 const Candidate kCandidates[] = {
@@ -248,6 +282,7 @@ int affon_rocm_session_create(int device, affon_rocm_session** out) {
   auto* session = new affon_rocm_session;
   session->device = device;
   session->stream = stream;
+  session->workspace = new affon::Workspace(device, stream);
   *out = session;
   return AFFON_ROCM_OK;
 }
@@ -259,8 +294,11 @@ int affon_rocm_session_destroy(affon_rocm_session* session) {
   if (hipSetDevice(session->device) == hipSuccess && session->stream != nullptr) {
     hipError_t e = hipStreamSynchronize(session->stream);
     if (e != hipSuccess) status = hip_fail(e, "hipStreamSynchronize");
+    delete session->workspace;
     e = hipStreamDestroy(session->stream);
     if (e != hipSuccess && status == AFFON_ROCM_OK) status = hip_fail(e, "hipStreamDestroy");
+  } else {
+    delete session->workspace;
   }
   delete session;
   return status;
@@ -337,7 +375,10 @@ int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qm
   const Candidate* c = nullptr;
   if ((status = select(desc, p, &c)) != AFFON_ROCM_OK) return status;
   if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
-  hipError_t e = c->launch(p, session->stream);
+  affon::Launch launch;
+  launch.stream = session->stream;
+  launch.workspace = session->workspace;
+  hipError_t e = c->launch(p, launch);
   if (e != hipSuccess) return hip_fail(e, c->id);
   return AFFON_ROCM_OK;
 }

@@ -14,6 +14,7 @@
 // MFMA B fragments in registers (codes -> f32 via FP8 conversion for 2/4-bit
 // or v_cvt_f32_ubyte for 8-bit -> s*q + b -> bf16).
 
+#include <mutex>
 #include <type_traits>
 
 #include "device.h"
@@ -27,6 +28,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128;                       // tile rows (activations)
 constexpr int kBN = 256;                       // tile columns (weights), 64 per wave
@@ -49,6 +51,11 @@ struct GemmArgs {
   float* out;  // [M, N]
   int M, N, K;
   int group_shift;  // log2(group / 32): groups of 32, 64, 128, ...
+  // Split of K over workgroups: splits ranges of split_steps K steps each.
+  // With splits > 1 each range writes its sums to partial [splits, M, N] f32
+  // and reduce_partials_kernel forms the output.
+  int splits, split_steps;
+  float* partial;
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -58,52 +65,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;
-}
-
-// Decodes 32 consecutive weights (words[] holds BITS words) with w = s*q + b
-// into four bf16x8 fragments (weights 8f .. 8f+7 in fragment f).
-template <int BITS>
-__device__ __forceinline__ void decode32(const uint32_t* words, float s, float b, bf16x8_t* frag) {
-  uint32_t pairs[16];
-  if constexpr (BITS == 8) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t v = opaque(words[i]);
-      float w[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w[j] = fmaf(static_cast<float>((v >> (8 * j)) & 0xffu), s, b);
-      pairs[2 * i] = pack_bf16(w[0], w[1]);
-      pairs[2 * i + 1] = pack_bf16(w[2], w[3]);
-    }
-  } else {
-    // FP8 conversion of bytes holding codes < 16: exactly n * 2^-9 (the
-    // caller passes s already multiplied by 2^9).
-    constexpr int P = 32 / BITS;
-    constexpr int T = BITS == 4 ? 2 : 4;
-    constexpr uint32_t kMask = BITS == 4 ? 0x0f0f0f0fu : 0x03030303u;
-#pragma unroll
-    for (int i = 0; i < BITS; ++i) {  // BITS words per 32 values
-      const uint32_t word = words[i];
-      float w[P];
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const uint32_t m = (word >> (BITS * t)) & kMask;
-        const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(m, false);  // bytes 0, 1
-        const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(m, true);   // bytes 2, 3
-        const float q[4] = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = BITS == 4 ? 2 * j + t : 4 * j + t;  // code position of byte j of mask t
-          w[k] = fmaf(q[j], s, b);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < P / 2; ++j) pairs[i * (P / 2) + j] = pack_bf16(w[2 * j], w[2 * j + 1]);
-    }
-  }
-#pragma unroll
-  for (int f = 0; f < 4; ++f)
-    frag[f] = __builtin_bit_cast(bf16x8_t, make_uint4(pairs[4 * f], pairs[4 * f + 1], pairs[4 * f + 2], pairs[4 * f + 3]));
 }
 
 // Waits until at most N vector-memory operations of this wave are in flight.
@@ -317,15 +278,22 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   const int li = lane & 31;
   const int lh = lane >> 5;
 
-  // Tile of this block: consecutive blocks go to consecutive XCDs, so the
-  // block index is remapped to give each XCD a contiguous run of tiles.
+  // Work unit of this block (tile, K range): consecutive blocks go to
+  // consecutive XCDs, so the block index is remapped to give each XCD a
+  // contiguous run of units (same K range, neighbouring tiles).
   const int nb_n = (a.N + kBN - 1) / kBN;
-  const int total = nb_n * ((a.M + kBM - 1) / kBM);
-  int tile = blockIdx.x;
-  if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
+  const int tiles = nb_n * ((a.M + kBM - 1) / kBM);
+  const int units = tiles * a.splits;
+  int unit = blockIdx.x;
+  if ((units & 7) == 0) unit = (unit & 7) * (units >> 3) + (unit >> 3);
+  const int split = unit / tiles;
+  const int tile = unit % tiles;
   const int m0 = (tile / nb_n) * kBM;
   const int n0 = (tile % nb_n) * kBN + 64 * wave;  // this wave's first column
-  const int steps = a.K / kBK;
+  // Steps below are local to the K range; s0 is its first global step
+  // (a multiple of 4, so local and global steps agree mod 4).
+  const int steps = a.split_steps;
+  const int s0 = split * steps;
   const int last = steps - 1;
 
   // Activation transfers: this wave fills 8-row groups g = kAGroupsPerWave*wave + i.
@@ -370,15 +338,15 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   // instruction j of the transfer starting at `step`; activation group i of `step`.
   auto issue_p = [&](int step, int i) {
     const uint32_t dst = lds_address(lds_p[(step >> 2) & 1][wave]) + (i < 4 ? 256 * i : 1024 + 256 * (i - 4));
-    const int off = 4 * min(window(step) + (lane & 3), row_dwords - 1);
+    const int off = 4 * min(window(s0 + step) + (lane & 3), row_dwords - 1);
     load_lds<4>((i < 4 ? s_col[i] : b_col[i - 4]) + off, dst);
   };
   auto issue_w = [&](int step, int j) {
     const int buf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
-    load_lds<16>(w_src[j] + static_cast<int64_t>(step) * (8 * BITS), lds_address(lds_w[buf][wave]) + 1024 * j);
+    load_lds<16>(w_src[j] + static_cast<int64_t>(s0 + step) * (8 * BITS), lds_address(lds_w[buf][wave]) + 1024 * j);
   };
   auto issue_a = [&](int step, int i) {
-    load_lds<16>(a_src[i] + step * kBK, lds_address(lds_a[step & 3]) + 1024 * (kAGroupsPerWave * wave + i));
+    load_lds<16>(a_src[i] + (s0 + step) * kBK, lds_address(lds_a[step & 3]) + 1024 * (kAGroupsPerWave * wave + i));
   };
   // All transfers of the iteration with index j, in the order the waits count them.
   auto issue_all = [&](int j, int pstep, int wstep, int astep) {
@@ -396,7 +364,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
     const int wbuf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
     const int sub = P::kStepsPerW == 1 ? 0 : (step & 3);  // step within the transfer
     // Position of this lane's group in the parameter window.
-    const int g = ((step * kBK + 32 * lh) >> (5 + a.group_shift)) - window(step & ~3) * (4 / PT::bytes);
+    const int g = (((s0 + step) * kBK + 32 * lh) >> (5 + a.group_shift)) - window(s0 + (step & ~3)) * (4 / PT::bytes);
     const uint8_t* pbuf = lds_p[(step >> 2) & 1][wave];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -514,25 +482,85 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
 
   // Accumulator (mt, nt) element v of lane l is row 8*(v/4) + 4*(l/32) + v%4
   // and column l%32 of its 32x32 tile.
+  auto for_each_output = [&](auto&& f) {
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int col = n0 + 32 * nt + li;
-    if (col >= a.N) continue;
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = n0 + 32 * nt + li;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
-        if (row < a.M) a.out[static_cast<int64_t>(row) * a.N + col] = acc[mt][nt][v];
-      }
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
+          if (row < a.M && col < a.N) f(static_cast<int64_t>(row) * a.N + col, acc[mt][nt][v]);
+        }
+    }
+  };
+  float* dst = a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N;
+  for_each_output([&](int64_t i, float v) { dst[i] = v; });
+}
+
+// out[i] = sum of the K ranges' partial sums, added in range order (the same
+// result on every run). Four outputs per thread; `count` = M*N; `vec` when
+// count % 4 == 0 and out is 16-byte aligned (partial always is).
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* partial, float* out, int64_t count,
+                                                              int splits, int vec) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= count) return;
+  if (vec) {
+    f32x4_t sum = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + i));
+    for (int r = 1; r < splits; ++r) sum += __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + r * count + i));
+    *reinterpret_cast<f32x4_t*>(out + i) = sum;
+  } else {
+    for (int64_t j = i; j < i + 4 && j < count; ++j) {
+      float sum = partial[j];
+      for (int r = 1; r < splits; ++r) sum += partial[r * count + j];
+      out[j] = sum;
+    }
   }
 }
 
 template <int BITS, typename PT>
 hipError_t launch_typed(const GemmArgs& args, hipStream_t stream) {
   const int tiles = ((args.N + kBN - 1) / kBN) * ((args.M + kBM - 1) / kBM);
-  hipLaunchKernelGGL((qgemm_kernel<BITS, PT>), dim3(tiles), dim3(kThreads), 0, stream, args);
+  hipLaunchKernelGGL((qgemm_kernel<BITS, PT>), dim3(tiles * args.splits), dim3(kThreads), 0, stream, args);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || args.splits == 1) return e;
+  const int64_t count = static_cast<int64_t>(args.M) * args.N;
+  const int64_t blocks = (count + 1023) / 1024;
+  const int vec = count % 4 == 0 && reinterpret_cast<uintptr_t>(args.out) % 16 == 0;
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                     args.partial, args.out, count, args.splits, vec);
   return hipGetLastError();
+}
+
+int device_cus() {
+  static std::mutex mutex;
+  static int cached[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mutex);
+  if (cached[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
+    cached[device] = cus;
+  }
+  return cached[device];
+}
+
+// Number of K ranges: 1 when the tiles alone fill three quarters of the CUs;
+// otherwise the smallest count of equal 4-step-aligned ranges (at most 8, at
+// least 8 steps each) that does, or the largest allowed.
+int choose_splits(int tiles, int steps) {
+  const int target = device_cus() * 3 / 4;
+  int splits = 1;
+  if (tiles >= target) return 1;
+  for (int s = 2; s <= 8; ++s) {
+    if ((steps / 4) % s != 0) continue;
+    if (steps / s < 8) break;
+    splits = s;
+    if (tiles * s >= target) break;
+  }
+  return splits;
 }
 
 }  // namespace
@@ -557,7 +585,8 @@ bool mfma_supports(const QmmProblem& p) {
   return true;
 }
 
-hipError_t mfma_launch(const QmmProblem& p, hipStream_t stream) {
+hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
+  hipStream_t stream = l.stream;
   GemmArgs a;
   a.x = reinterpret_cast<const uint16_t*>(p.x);
   a.xs0 = p.xs0;
@@ -573,6 +602,19 @@ hipError_t mfma_launch(const QmmProblem& p, hipStream_t stream) {
   a.K = static_cast<int>(p.K);
   a.group_shift = 0;
   while ((int64_t(32) << a.group_shift) < p.group) ++a.group_shift;
+  const int tiles = static_cast<int>(((p.N + kBN - 1) / kBN) * ((p.M + kBM - 1) / kBM));
+  const int steps = static_cast<int>(p.K / kBK);
+  a.splits = 1;
+  a.split_steps = steps;
+  a.partial = nullptr;
+  const int splits = l.workspace != nullptr ? choose_splits(tiles, steps) : 1;
+  if (splits > 1) {
+    if (auto* ws = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * p.N * 4))) {
+      a.splits = splits;
+      a.split_steps = steps / splits;
+      a.partial = ws;
+    }
+  }
   const bool bf16p = p.p_dtype == AFFON_ROCM_BF16;
   switch (p.bits) {
     case 2: return bf16p ? launch_typed<2, BF16>(a, stream) : launch_typed<2, F32>(a, stream);
@@ -582,6 +624,6 @@ hipError_t mfma_launch(const QmmProblem& p, hipStream_t stream) {
 }
 
 bool gemv_mfma_supports(const QmmProblem&) { return false; }
-hipError_t gemv_mfma_launch(const QmmProblem&, hipStream_t) { return hipErrorNotSupported; }
+hipError_t gemv_mfma_launch(const QmmProblem&, const Launch&) { return hipErrorNotSupported; }
 
 }  // namespace affon

@@ -274,7 +274,8 @@ bool gemv1_supports(const QmmProblem& p) {
   return lds <= gemv1::kMaxLdsBytes && chunks <= gemv1::kMaxChunks;
 }
 
-hipError_t gemv_launch(const QmmProblem& p, hipStream_t stream) {
+hipError_t gemv_launch(const QmmProblem& p, const Launch& l) {
+  hipStream_t stream = l.stream;
   if (gemv1_supports(p)) {
     switch (p.bits) {
       case 2: return gemv1_launch_b2(p, stream);

@@ -60,7 +60,8 @@ bool generic_supports(const QmmProblem& p) {
   return p.M * p.N <= (int64_t(1) << 38);
 }
 
-hipError_t generic_launch(const QmmProblem& p, hipStream_t stream) {
+hipError_t generic_launch(const QmmProblem& p, const Launch& l) {
+  hipStream_t stream = l.stream;
   const int64_t total = p.M * p.N;
   const dim3 block(256);
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));

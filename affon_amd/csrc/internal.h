@@ -27,20 +27,44 @@ struct QmmProblem {
   float* out = nullptr;
 };
 
+// Device scratch memory owned by a session and ordered by its stream.
+class Workspace {
+ public:
+  Workspace(int device, hipStream_t stream) : device_(device), stream_(stream) {}
+  ~Workspace();
+  Workspace(const Workspace&) = delete;
+  Workspace& operator=(const Workspace&) = delete;
+  // At least `bytes` of device memory, or nullptr when it cannot grow now
+  // (the stream is being captured into a graph, or the allocation failed).
+  void* get(size_t bytes);
+
+ private:
+  int device_;
+  hipStream_t stream_;
+  void* ptr_ = nullptr;
+  size_t bytes_ = 0;
+};
+
+// Where a launcher enqueues its work.
+struct Launch {
+  hipStream_t stream = nullptr;
+  Workspace* workspace = nullptr;  // may be null: launchers then use no scratch memory
+};
+
 // Per-candidate capability guards and launchers. A guard returns true when
 // the candidate can run the problem (shape, layout, alignment); launchers
 // enqueue on the given stream and return the launch status.
 bool generic_supports(const QmmProblem& p);
-hipError_t generic_launch(const QmmProblem& p, hipStream_t stream);
+hipError_t generic_launch(const QmmProblem& p, const Launch& l);
 
 bool gemv_supports(const QmmProblem& p);
-hipError_t gemv_launch(const QmmProblem& p, hipStream_t stream);
+hipError_t gemv_launch(const QmmProblem& p, const Launch& l);
 
 bool gemv_mfma_supports(const QmmProblem& p);
-hipError_t gemv_mfma_launch(const QmmProblem& p, hipStream_t stream);
+hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l);
 
 bool mfma_supports(const QmmProblem& p);
-hipError_t mfma_launch(const QmmProblem& p, hipStream_t stream);
+hipError_t mfma_launch(const QmmProblem& p, const Launch& l);
 
 hipError_t quantize_launch(const void* weights, int weight_dtype, int64_t rows, int64_t columns,
                            int bits, int64_t group, uint32_t* packed, void* scales, void* biases,

@@ -389,6 +389,23 @@ def test_prefill_seeded_against_oracle(session, bits, group):
         check_against_oracle(run_mfma(session, xt, wt, st, bt, bits, group), x, packed, s, b, bits, group, True)
 
 
+def test_prefill_split_k_deterministic(session):
+    """Shapes with few tiles split K over workgroups (partials summed in range
+    order by the last arrival): repeated runs are bit-identical, and match the
+    reassociated decode kernel within the bf16 tolerance."""
+    for M, N, K, bits, group in [(512, 4096, 14336, 4, 64), (64, 256, 4096, 8, 64), (300, 300, 1024, 2, 128)]:
+        x, packed, s, b = seeded_problem(M, N, K, bits, group, "bf16", "bf16", seed=11)
+        xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+        first = run_mfma(session, xt, wt, st, bt, bits, group)
+        for _ in range(3):
+            np.testing.assert_array_equal(run_mfma(session, xt, wt, st, bt, bits, group), first)
+        ref = session.empty("f32", (M, N))
+        A.quantized_matmul_into(ref, xt, wt, st, bt, bits=bits, group_size=group, implementation="gemv")
+        ref = ref.numpy()
+        rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+        assert_close_rtol_atol(first, ref, rtol=1e-2, atol=1e-2 * rms)
+
+
 @pytest.mark.parametrize("shape", [(512, 14336, 4096, 4, 64), (512, 4096, 14336, 4, 64)])
 def test_prefill_full_size_against_exact_kernel(session, shape):
     """Full prefill shapes: every output element against the reassociated
