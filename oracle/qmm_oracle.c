@@ -18,11 +18,18 @@
  *                                non-integer inputs is parity unpinned (its source is
  *                                not in the reference tree); parity there is by tolerance.
  *   oracle_quantized_matmul_f64  same checks in f64.
- *   oracle_bf16_from_f32         exhaustive comparison over all 2^32 patterns with
- *                                the reference's RNE formula (probe-capabilities.py:112-115).
- *   oracle_randn / mulberry32    first values of the stream checked against values
- *                                derived by hand from program.ts:1385-1426 arithmetic
- *                                and against distribution moments.
+ *   oracle_bf16_from_f32         every upper half-word combined with the low halves that
+ *                                decide rounding (ties, both sides, extremes) against the
+ *                                reference's RNE formula (probe-capabilities.py:112-115),
+ *                                and 300,000 values (random, subnormal, random bit patterns)
+ *                                against torch's float32 -> bfloat16 conversion.
+ *   oracle_randn / mulberry32    the uniform stream for six seeds against an independent
+ *                                restatement of program.ts:1385-1394 with JS int32 semantics
+ *                                written out (Math.imul, ToInt32); Box-Muller pairing and
+ *                                moments. The f64 log/sin/cos come from libm here and from
+ *                                V8 in the reference: bit-level agreement of every normal is
+ *                                parity unpinned (a last-ulp f64 difference almost never
+ *                                survives the rounding to f32).
  *   oracle_quantize              build-defined contract (no reference op exists):
  *                                invariants q in range, group min -> 0, group max -> 2^bits-1,
  *                                |dequant - w| <= scale/2 (+ bf16 parameter rounding),
