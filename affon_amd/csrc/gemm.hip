@@ -14,102 +14,17 @@
 // MFMA B fragments in registers (codes -> f32 via FP8 conversion for 2/4-bit
 // or v_cvt_f32_ubyte for 8-bit -> s*q + b -> bf16).
 
-#include <mutex>
-#include <type_traits>
-
-#include "device.h"
-#include "internal.h"
+#include "lds_pipeline.h"
 
 namespace affon {
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+using namespace pipeline;
 
 constexpr int kBM = 128;                       // tile rows (activations)
 constexpr int kBN = 256;                       // tile columns (weights), 64 per wave
-constexpr int kBK = 64;                        // K step
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kStages = 4;                     // LDS ring depth (steps)
 constexpr int kAStageBytes = kBM * kBK * 2;    // 16 KiB: 128 rows x 128 bytes
 constexpr int kAGroupsPerWave = kBM / 8 / kWaves;  // 8-row DMA groups per wave
-
-struct GemmArgs {
-  const uint16_t* x;  // bf16 [M, K], row stride xs0 elements
-  int64_t xs0;
-  const uint32_t* w;  // packed [N, K/P], row stride ws0 words
-  int64_t ws0;
-  const uint8_t* s;
-  int64_t ss0;
-  const uint8_t* b;
-  int64_t bs0;
-  float* out;  // [M, N]
-  int M, N, K;
-  int group_shift;  // log2(group / 32): groups of 32, 64, 128, ...
-  // Split of K over workgroups: splits ranges of split_steps K steps each.
-  // With splits > 1 each range writes its sums to partial [splits, M, N] f32
-  // and reduce_partials_kernel forms the output.
-  int splits, split_steps;
-  float* partial;
-};
-
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, bf16x2_t{static_cast<__bf16>(a), static_cast<__bf16>(b)});
-}
-
-__device__ __forceinline__ uint32_t opaque(uint32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-
-// Waits until at most N vector-memory operations of this wave are in flight.
-// Written as asm with a memory clobber so that no memory access moves across
-// it (the compiler does not see the direct-to-LDS loads it stands guard for).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// size bytes per lane (4 or 16) from global memory straight into LDS: lane
-// L's bytes land at lds_addr + size * L (lds_addr wave-uniform). Issued as
-// asm: the compiler would otherwise drain the load counter before every LDS
-// read it cannot prove disjoint from the transfer; here the caller orders them
-// with wait_vmcnt and a barrier.
-template <int SIZE>
-__device__ __forceinline__ void load_lds(const void* src, uint32_t lds_addr) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  if constexpr (SIZE == 16)
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
-#pragma clang diagnostic pop
-}
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
-}
-
-// Compile-time unrolled loop: f(std::integral_constant<int, I>) for I in [I0, N).
-template <int I, int N>
-struct Unroll {
-  template <class F>
-  __device__ __forceinline__ static void run(F&& f) {
-    f(std::integral_constant<int, I>{});
-    Unroll<I + 1, N>::run(f);
-  }
-};
-template <int N>
-struct Unroll<N, N> {
-  template <class F>
-  __device__ __forceinline__ static void run(F&&) {}
-};
 
 // Inputs of one step's decode for one lane: BITS packed words (32 weights)
 // and the raw parameter bits of each of the lane's two columns.
@@ -125,11 +40,6 @@ struct DecodeTmp {
   float s[2], b[2];
   f32x2_t lo[4], hi[4];
 };
-
-template <typename PT>
-__device__ __forceinline__ float widen_param(uint32_t raw) {
-  return PT::bytes == 2 ? __uint_as_float(raw << 16) : __uint_as_float(raw);
-}
 
 // Piece p (0..31) of a step's decode: the 64 weights of a lane (2 columns x
 // 32 k) split into 32 pieces of 5-6 VALU instructions, one per MFMA. Words
@@ -184,70 +94,6 @@ __device__ __forceinline__ void decode_piece(const DecodeIn<BITS>& in, DecodeTmp
   }
 }
 
-// Transfer plan of one wave (64 weight columns) for a weight format.
-//
-// Packed words reach LDS in runs of kColBytes per column: four K steps at a
-// time for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per column), one step at a
-// time for 8-bit (64 bytes) -- so each transfer instruction covers whole
-// half or full 128-byte lines. Inside a column run the 16-byte slots are
-// XOR-swizzled with the column index so that the decode's fragment reads
-// (lanes = consecutive columns) are bank-conflict free whether the LDS serves
-// 8 lanes x 16 bytes (128 bytes) or 16 lanes x 16 bytes (256 bytes) per cycle. Scales and biases come as one 16-byte window per
-// column every four steps (four lanes per column, one dword each; bf16: 8
-// groups, f32: 4 groups), starting at the dword that holds the first group of
-// those 256 k values, which covers all of their groups for the group sizes
-// the kernel accepts; dwords past the row end repeat the row's last dword.
-template <int BITS, typename PT>
-struct Plan {
-  static constexpr int kStepsPerW = BITS == 8 ? 1 : 4;           // steps per packed-word transfer
-  static constexpr int kColBytes = 8 * BITS * kStepsPerW;         // bytes per column per transfer
-  static constexpr int kSlots = kColBytes / 16;                   // 16-byte slots per column run
-  static constexpr int kWLoads = 64 * kColBytes / 1024;           // 16-byte DMA instructions per transfer
-  static constexpr int kWBytes = 64 * kColBytes;                  // per wave and buffer
-  static constexpr int kWBufs = kStepsPerW == 1 ? kStages : 2;    // ring depth (buffers)
-  static constexpr int kPLoads = 8;                               // 4-byte DMA: 4 for scales, 4 for biases
-  static constexpr int kPBytes = 2 * 64 * 16;                     // per wave and buffer: 16-byte windows of scales, biases
-  static constexpr int kALoads = kAGroupsPerWave;
-
-  // Slot (16-byte unit) holding part `part` of column c's run. 128-byte runs:
-  // within 8 consecutive columns the slots differ; columns c and c+8 (same
-  // 128-byte bank phase in a 256-byte window) differ in slot bit 0. 64-byte
-  // runs: even columns 0,2,4,6 (and odd 1,3,5,7) use different slots, and so
-  // do columns c, c+4, c+8, c+12.
-  static __device__ __forceinline__ int slot(int c, int part) {
-    return kSlots == 8 ? part ^ (c & 7) ^ ((c >> 3) & 1) : part ^ (((c >> 1) ^ (c >> 3)) & 3);
-  }
-
-  // Transfers issued by iteration j (= step index mod 4), in issue order
-  // parameters, words, activations; group 0 = parameters, 1 = words, 2 = activations.
-  static constexpr int group_ops(int j, int g) {
-    return g == 0 ? (j == 0 ? kPLoads : 0) : g == 1 ? (kStepsPerW == 1 || j == 0 ? kWLoads : 0) : kALoads;
-  }
-  static constexpr int ops(int j) { return group_ops(j, 0) + group_ops(j, 1) + group_ops(j, 2); }
-  // Transfers issued after group g of the iteration r iterations before one
-  // with index j, up to the start of that one.
-  static constexpr int ops_after(int j, int r, int g) {
-    const int jr = ((j - r) % 4 + 4) % 4;
-    int n = 0;
-    for (int h = g + 1; h < 3; ++h) n += group_ops(jr, h);
-    for (int i = 1; i < r; ++i) n += ops(((j - i) % 4 + 4) % 4);
-    return n;
-  }
-  // vmcnt bound at the start of iteration j: the activations of its step
-  // (issued three iterations before) and the words and parameters of the
-  // next step (decoded during it) must have landed.
-  static constexpr int wait(int j) {
-    int n = ops_after(j, 3, 2);
-    const int rw = kStepsPerW == 1 ? 3 : (j == 3 ? 3 : j + 4);
-    const int rp = j == 3 ? 3 : j + 4;
-    const int nw = ops_after(j, rw, 1), np = ops_after(j, rp, 0);
-    n = nw < n ? nw : n;
-    n = np < n ? np : n;
-    return n;
-  }
-  static_assert(kWLoads * 1024 == kWBytes, "whole DMA instructions");
-};
-
 // Workgroup tile 128 x 256, K step 64, four waves side by side along N (each
 // all 128 rows x 64 columns = 4 x 2 tiles of 32x32 accumulators). Blocks are
 // ordered so that the blocks one XCD runs share one row panel of activations
@@ -266,8 +112,8 @@ struct Plan {
 // its own transfers (no barrier needed for them); the barrier orders the
 // shared activation tile. Step t+1 is decoded while step t's MFMAs run.
 template <int BITS, typename PT>
-__global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
-  using P = Plan<BITS, PT>;
+__global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(TileArgs a) {
+  using P = Plan<BITS, PT, kAGroupsPerWave>;
   __shared__ __attribute__((aligned(16))) uint8_t lds_a[kStages][kAStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[P::kWBufs][kWaves][P::kWBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_p[2][kWaves][P::kPBytes];
@@ -278,16 +124,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   const int li = lane & 31;
   const int lh = lane >> 5;
 
-  // Work unit of this block (tile, K range): consecutive blocks go to
-  // consecutive XCDs, so the block index is remapped to give each XCD a
-  // contiguous run of units (same K range, neighbouring tiles).
   const int nb_n = (a.N + kBN - 1) / kBN;
-  const int tiles = nb_n * ((a.M + kBM - 1) / kBM);
-  const int units = tiles * a.splits;
-  int unit = blockIdx.x;
-  if ((units & 7) == 0) unit = (unit & 7) * (units >> 3) + (unit >> 3);
-  const int split = unit / tiles;
-  const int tile = unit % tiles;
+  int tile, split;
+  work_unit(nb_n * ((a.M + kBM - 1) / kBM), a.splits, &tile, &split);
   const int m0 = (tile / nb_n) * kBM;
   const int n0 = (tile % nb_n) * kBN + 64 * wave;  // this wave's first column
   // Steps below are local to the K range; s0 is its first global step
@@ -307,44 +146,10 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
     const int row = min(m0 + 8 * (kAGroupsPerWave * wave + i) + (lane >> 3), a.M - 1);
     a_src[i] = a.x + static_cast<int64_t>(row) * a.xs0 + 8 * ((lane & 7) ^ (lane >> 3) ^ (i & 1));
   }
-  // Packed-word transfers: DMA lane L of instruction j writes LDS byte
-  // 1024j + 16L of the wave's buffer = slot (16L % kColBytes) / 16 of local
-  // column (1024j + 16L) / kColBytes, which holds part slot ^ swizzle.
-  const uint8_t* w_src[P::kWLoads];
-#pragma unroll
-  for (int j = 0; j < P::kWLoads; ++j) {
-    const int pos = 1024 * j + 16 * lane;
-    const int c = pos / P::kColBytes;
-    const int part = P::slot(c, (pos % P::kColBytes) / 16);  // the swizzle is an involution
-    const int col = min(n0 + c, a.N - 1);  // columns past N feed unstored outputs
-    w_src[j] = reinterpret_cast<const uint8_t*>(a.w + static_cast<int64_t>(col) * a.ws0) + 16 * part;
-  }
-  // Parameter windows: DMA lane L of instruction i carries dword L%4 of the
-  // window of local column 16i + L/4, stored at byte 16*(16i + L/4) + 4*(L%4).
-  const int row_dwords = (a.K >> (5 + a.group_shift)) * PT::bytes / 4;  // whole dwords per parameter row
-  const uint8_t* s_col[4];
-  const uint8_t* b_col[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int col = min(n0 + 16 * i + (lane >> 2), a.N - 1);
-    s_col[i] = a.s + static_cast<int64_t>(col) * a.ss0 * PT::bytes;
-    b_col[i] = a.b + static_cast<int64_t>(col) * a.bs0 * PT::bytes;
-  }
-  // First dword of the window for the four steps starting at `step`.
-  auto window = [&](int step) { return (((step * kBK) >> (5 + a.group_shift)) * PT::bytes) >> 2; };
-
-  // Single transfer instructions: parameter window i (0..3 scales, 4..7
-  // biases) of the four steps starting at `step` (a multiple of 4); packed-word
-  // instruction j of the transfer starting at `step`; activation group i of `step`.
-  auto issue_p = [&](int step, int i) {
-    const uint32_t dst = lds_address(lds_p[(step >> 2) & 1][wave]) + (i < 4 ? 256 * i : 1024 + 256 * (i - 4));
-    const int off = 4 * min(window(s0 + step) + (lane & 3), row_dwords - 1);
-    load_lds<4>((i < 4 ? s_col[i] : b_col[i - 4]) + off, dst);
-  };
-  auto issue_w = [&](int step, int j) {
-    const int buf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
-    load_lds<16>(w_src[j] + static_cast<int64_t>(s0 + step) * (8 * BITS), lds_address(lds_w[buf][wave]) + 1024 * j);
-  };
+  WeightStream<BITS, PT, kAGroupsPerWave> ws;
+  ws.init(a, n0, s0, lane, lds_w[0][wave], kWaves * P::kWBytes, lds_p[0][wave], kWaves * P::kPBytes);
+  auto issue_p = [&](int step, int i) { ws.issue_p(step, i); };
+  auto issue_w = [&](int step, int j) { ws.issue_w(step, j); };
   auto issue_a = [&](int step, int i) {
     load_lds<16>(a_src[i] + (s0 + step) * kBK, lds_address(lds_a[step & 3]) + 1024 * (kAGroupsPerWave * wave + i));
   };
@@ -361,37 +166,24 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   // 32*lh .. 32*lh+31 of the step.
   const float code_scale = BITS == 8 ? 1.0f : 512.0f;
   auto load_decode = [&](int step, DecodeIn<BITS>& in) {
-    const int wbuf = P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1);
-    const int sub = P::kStepsPerW == 1 ? 0 : (step & 3);  // step within the transfer
-    // Position of this lane's group in the parameter window.
-    const int g = (((s0 + step) * kBK + 32 * lh) >> (5 + a.group_shift)) - window(s0 + (step & ~3)) * (4 / PT::bytes);
-    const uint8_t* pbuf = lds_p[(step >> 2) & 1][wave];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int c = 32 * nt + li;
-      const uint8_t* col = lds_w[wbuf][wave] + c * P::kColBytes;
-      if constexpr (BITS == 2) {  // 8 bytes: half of slot `sub`
-        const uint2 v = *reinterpret_cast<const uint2*>(col + 16 * P::slot(c, sub) + 8 * lh);
+      if constexpr (BITS == 2) {  // 8 bytes: half of the step's 16-byte part
+        const uint2 v = *reinterpret_cast<const uint2*>(ws.w_part(step, c, 0) + 8 * lh);
         in.words[nt][0] = v.x;
         in.words[nt][1] = v.y;
       } else {
 #pragma unroll
-        for (int i = 0; i < BITS / 4; ++i) {  // 4-bit: part 2*sub + lh; 8-bit: parts 2*lh, 2*lh + 1
-          const int part = BITS == 4 ? 2 * sub + lh : 2 * lh + i;
-          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(col + 16 * P::slot(c, part));
+        for (int i = 0; i < BITS / 4; ++i) {  // 4-bit: part lh; 8-bit: parts 2*lh, 2*lh + 1
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ws.w_part(step, c, BITS == 4 ? lh : 2 * lh + i));
           in.words[nt][4 * i] = v.x;
           in.words[nt][4 * i + 1] = v.y;
           in.words[nt][4 * i + 2] = v.z;
           in.words[nt][4 * i + 3] = v.w;
         }
       }
-      if constexpr (PT::bytes == 2) {
-        in.s_raw[nt] = *reinterpret_cast<const uint16_t*>(pbuf + 16 * c + 2 * g);
-        in.b_raw[nt] = *reinterpret_cast<const uint16_t*>(pbuf + 1024 + 16 * c + 2 * g);
-      } else {
-        in.s_raw[nt] = *reinterpret_cast<const uint32_t*>(pbuf + 16 * c + 4 * g);
-        in.b_raw[nt] = *reinterpret_cast<const uint32_t*>(pbuf + 1024 + 16 * c + 4 * g);
-      }
+      ws.params(step, c, 32 * lh, &in.s_raw[nt], &in.b_raw[nt]);
     }
   };
 
@@ -499,68 +291,13 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(GemmArgs a) {
   for_each_output([&](int64_t i, float v) { dst[i] = v; });
 }
 
-// out[i] = sum of the K ranges' partial sums, added in range order (the same
-// result on every run). Four outputs per thread; `count` = M*N; `vec` when
-// count % 4 == 0 and out is 16-byte aligned (partial always is).
-__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* partial, float* out, int64_t count,
-                                                              int splits, int vec) {
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
-  if (i >= count) return;
-  if (vec) {
-    f32x4_t sum = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + i));
-    for (int r = 1; r < splits; ++r) sum += __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + r * count + i));
-    *reinterpret_cast<f32x4_t*>(out + i) = sum;
-  } else {
-    for (int64_t j = i; j < i + 4 && j < count; ++j) {
-      float sum = partial[j];
-      for (int r = 1; r < splits; ++r) sum += partial[r * count + j];
-      out[j] = sum;
-    }
-  }
-}
-
 template <int BITS, typename PT>
-hipError_t launch_typed(const GemmArgs& args, hipStream_t stream) {
+hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
   const int tiles = ((args.N + kBN - 1) / kBN) * ((args.M + kBM - 1) / kBM);
   hipLaunchKernelGGL((qgemm_kernel<BITS, PT>), dim3(tiles * args.splits), dim3(kThreads), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || args.splits == 1) return e;
-  const int64_t count = static_cast<int64_t>(args.M) * args.N;
-  const int64_t blocks = (count + 1023) / 1024;
-  const int vec = count % 4 == 0 && reinterpret_cast<uintptr_t>(args.out) % 16 == 0;
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     args.partial, args.out, count, args.splits, vec);
-  return hipGetLastError();
-}
-
-int device_cus() {
-  static std::mutex mutex;
-  static int cached[64] = {0};
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
-  std::lock_guard<std::mutex> lock(mutex);
-  if (cached[device] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
-    cached[device] = cus;
-  }
-  return cached[device];
-}
-
-// Number of K ranges: 1 when the tiles alone fill three quarters of the CUs;
-// otherwise the smallest count of equal 4-step-aligned ranges (at most 8, at
-// least 8 steps each) that does, or the largest allowed.
-int choose_splits(int tiles, int steps) {
-  const int target = device_cus() * 3 / 4;
-  int splits = 1;
-  if (tiles >= target) return 1;
-  for (int s = 2; s <= 8; ++s) {
-    if ((steps / 4) % s != 0) continue;
-    if (steps / s < 8) break;
-    splits = s;
-    if (tiles * s >= target) break;
-  }
-  return splits;
+  return launch_reduce(args, stream);
 }
 
 }  // namespace
@@ -587,7 +324,7 @@ bool mfma_supports(const QmmProblem& p) {
 
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
   hipStream_t stream = l.stream;
-  GemmArgs a;
+  TileArgs a;
   a.x = reinterpret_cast<const uint16_t*>(p.x);
   a.xs0 = p.xs0;
   a.w = p.w;
@@ -623,7 +360,5 @@ hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
   }
 }
 
-bool gemv_mfma_supports(const QmmProblem&) { return false; }
-hipError_t gemv_mfma_launch(const QmmProblem&, const Launch&) { return hipErrorNotSupported; }
 
 }  // namespace affon

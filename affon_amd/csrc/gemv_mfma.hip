@@ -1,0 +1,286 @@
+// rocm_quantized_matmul.gemv_mfma — decode batches (M <= 16) with bf16
+// activations on the matrix cores.
+//
+// Counterpart of the reference's small-M decode variants (metal simd4 /
+// matrix32 by M, docs/core/quantized-inference.md:132-140,151-170). Numerical
+// class "reassociated": the packed codes q are exact integers in bf16, so
+// v_mfma_f32_16x16x32_bf16 forms each K step's sums sum(x*q) with f32
+// accumulation and no rounding of decoded weights; every K step (64 k) lies
+// in one group, and the group's scale and bias are applied in f32 to the
+// step sums: y += s * sum(x*q) + b * sum(x) -- the arithmetic of the VALU
+// decode kernel, with sum(x) from one more MFMA against a bf16 ones operand.
+//
+// Work mapping: a 16 x 256 tile per workgroup (rows past M repeat row M-1
+// and are not stored), four waves side by side along N with 4 MFMA column
+// tiles of 16 each, K split over workgroups when the tiles alone cannot fill
+// the GPU. Operands reach LDS by the same direct transfers, ring and counted
+// waits as the prefill GEMM (lds_pipeline.h).
+
+#include "lds_pipeline.h"
+
+namespace affon {
+namespace {
+
+using namespace pipeline;
+
+constexpr int kRows = 16;                        // activation rows per tile
+constexpr int kCols = 256;                       // weight columns per tile
+constexpr int kXStageBytes = kRows * kBK * 2;    // 2 KiB: 16 rows x 128 bytes
+constexpr int kXLoads = 1;                       // activation DMA instructions per wave and step
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Bytes 0,1 (HIGH false) or 2,3 (HIGH true) of `bytes` read as FP8 E4M3,
+// converted to a bf16 pair.
+template <bool HIGH>
+__device__ __forceinline__ uint32_t bf16_pair_fp8(uint32_t bytes) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, 1.0f, HIGH));
+}
+
+// B operands of MFMA t = 0, 1 for one lane and column: the lane's 16 codes of
+// the step (k = 16h .. 16h+15, h = lane / 16) in `words`, codes 8t .. 8t+7
+// into operand t as bf16. 2/4-bit codes go through the FP8 conversion (a
+// byte holding n < 16 reads as n * 2^-9, exactly; the scale carries 2^9),
+// 8-bit codes through v_cvt_f32_ubyteN (exact in bf16 up to 255).
+template <int BITS>
+__device__ __forceinline__ void codes_bf16(const uint32_t* words, u32x4_t* op) {
+  if constexpr (BITS == 4) {  // word t = codes 8t .. 8t+7, code i in nibble i
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t w = words[t];
+      const uint32_t even = w & 0x0f0f0f0fu;         // byte j = code 2j
+      const uint32_t odd = (w >> 4) & 0x0f0f0f0fu;   // byte j = code 2j+1
+      const uint32_t lo = __builtin_amdgcn_perm(odd, even, 0x05010400u);  // codes 0,1,2,3
+      const uint32_t hi = __builtin_amdgcn_perm(odd, even, 0x07030602u);  // codes 4,5,6,7
+      op[t] = u32x4_t{bf16_pair_fp8<false>(lo), bf16_pair_fp8<true>(lo), bf16_pair_fp8<false>(hi),
+                      bf16_pair_fp8<true>(hi)};
+    }
+  } else if constexpr (BITS == 2) {  // one word, code i at bits 2i
+    const uint32_t w = words[0];
+    uint32_t m[4];  // byte j of m[u] = code 4j + u
+#pragma unroll
+    for (int u = 0; u < 4; ++u) m[u] = (w >> (2 * u)) & 0x03030303u;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      // bytes 2t, 2t+1 of m[u] hold codes 8t+u and 8t+4+u.
+      const uint32_t sel = (2 * t) | ((4 + 2 * t) << 8) | ((2 * t + 1) << 16) | ((5 + 2 * t) << 24);
+      const uint32_t q01 = __builtin_amdgcn_perm(m[1], m[0], sel);  // codes 8t, 8t+1, 8t+4, 8t+5
+      const uint32_t q23 = __builtin_amdgcn_perm(m[3], m[2], sel);  // codes 8t+2, 8t+3, 8t+6, 8t+7
+      const uint32_t lo = __builtin_amdgcn_perm(q23, q01, 0x05040100u);  // codes 8t .. 8t+3
+      const uint32_t hi = __builtin_amdgcn_perm(q23, q01, 0x07060302u);  // codes 8t+4 .. 8t+7
+      op[t] = u32x4_t{bf16_pair_fp8<false>(lo), bf16_pair_fp8<true>(lo), bf16_pair_fp8<false>(hi),
+                      bf16_pair_fp8<true>(hi)};
+    }
+  } else {  // words 2t, 2t+1 = codes 8t .. 8t+7, one byte each
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      uint32_t pairs[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t v = opaque(words[2 * t + i]);
+        pairs[2 * i] = pack_bf16(static_cast<float>(v & 0xffu), static_cast<float>((v >> 8) & 0xffu));
+        pairs[2 * i + 1] = pack_bf16(static_cast<float>((v >> 16) & 0xffu), static_cast<float>(v >> 24));
+      }
+      op[t] = u32x4_t{pairs[0], pairs[1], pairs[2], pairs[3]};
+    }
+  }
+}
+
+// Workgroup tile 16 x 256, K step 64 (one group or part of one), four waves
+// side by side along N, each 16 rows x 64 columns = 4 column tiles.
+//
+// K order inside a step: MFMA t of lane quarter h (lanes 16h .. 16h+15)
+// covers k = 16h + 8t .. 16h + 8t + 7, for both operands, so a lane's codes
+// for the step are one contiguous run of 16 and every MFMA stays inside the
+// step. The 16 activation rows of a step sit in LDS as 16-byte chunks, chunk
+// c of row r at slot c ^ (r%8) ^ ((r/8)%2) (conflict-free fragment reads);
+// wave w transfers rows 4w .. 4w+3 (one DMA instruction, lanes 0..31).
+template <int BITS, typename PT>
+__global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
+  using P = Plan<BITS, PT, kXLoads>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_x[kStages][kXStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_w[P::kWBufs][kWaves][P::kWBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_p[2][kWaves][P::kPBytes];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int r = lane & 15;   // row of the A operand and column of the B operand and output
+  const int h = lane >> 4;   // lane quarter
+
+  const int nb_n = (a.N + kCols - 1) / kCols;
+  int tile, split;
+  work_unit(nb_n, a.splits, &tile, &split);
+  const int n0 = tile * kCols + 64 * wave;  // this wave's first column
+  const int steps = a.split_steps;
+  const int s0 = split * steps;
+  const int last = steps - 1;
+
+  // Activation transfer: lane L < 32 writes slot L%8 of row 4w + L/8.
+  const int xrow = 4 * wave + ((lane >> 3) & 3);
+  const uint16_t* x_src = a.x + static_cast<int64_t>(min(xrow, a.M - 1)) * a.xs0 +
+                          8 * ((lane & 7) ^ (xrow & 7) ^ ((xrow >> 3) & 1));
+  auto issue_a = [&](int step, int) {
+    if (lane < 32) load_lds<16>(x_src + (s0 + step) * kBK, lds_address(lds_x[step & 3]) + 512 * wave);
+  };
+  WeightStream<BITS, PT, kXLoads> ws;
+  ws.init(a, n0, s0, lane, lds_w[0][wave], kWaves * P::kWBytes, lds_p[0][wave], kWaves * P::kPBytes);
+  auto issue_all = [&](int j, int pstep, int wstep, int astep) {
+    if (j == 0)
+      for (int i = 0; i < P::kPLoads; ++i) ws.issue_p(pstep, i);
+    if (P::kStepsPerW == 1 || j == 0)
+      for (int i = 0; i < P::kWLoads; ++i) ws.issue_w(wstep, i);
+    issue_a(astep, 0);
+  };
+  // A operand of MFMA t: row r, chunk 2h + t.
+  auto read_x = [&](int stage, int t) -> bf16x8_t {
+    const int slot = (2 * h + t) ^ (r & 7) ^ ((r >> 3) & 1);
+    return *reinterpret_cast<const bf16x8_t*>(&lds_x[stage][(r >> 3) * 1024 + (8 * (r & 7) + slot) * 16]);
+  };
+  // The lane's 16 codes of column c (local) for `step`.
+  auto read_codes = [&](int step, int c, uint32_t* words) {
+    if constexpr (BITS == 2) {
+      words[0] = *reinterpret_cast<const uint32_t*>(ws.w_part(step, c, 0) + 4 * h);
+    } else if constexpr (BITS == 4) {
+      const u32x2_t v = *reinterpret_cast<const u32x2_t*>(ws.w_part(step, c, h >> 1) + 8 * (h & 1));
+      words[0] = v.x;
+      words[1] = v.y;
+    } else {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ws.w_part(step, c, h));
+      words[0] = v.x;
+      words[1] = v.y;
+      words[2] = v.z;
+      words[3] = v.w;
+    }
+  };
+
+  const float code_scale = BITS == 8 ? 1.0f : 512.0f;
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+  f32x4_t y[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) y[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Transfers exactly as the prefill GEMM orders them (Plan<..., kXLoads>):
+  // iterations -4 .. -1 issue the prologue, iteration t issues parameters and
+  // words at t%4 == 0 (2/4-bit) or every step (8-bit words), then the
+  // activations of step t+3. Step t is decoded in iteration t from LDS reads
+  // that complete before that iteration's transfers are issued: the 8-bit
+  // words of step t+4 reuse step t's buffer.
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) issue_all(rr, 0, min(rr, last), min(max(rr - 1, 0), last));
+
+#define AFFON_QSKINNY_STEP(J)                                                                            \
+  {                                                                                                      \
+    wait_vmcnt<P::wait(J)>();                                                                            \
+    __syncthreads();                                                                                     \
+    const bf16x8_t x0 = read_x((J), 0), x1 = read_x((J), 1);                                             \
+    uint32_t words[4][BITS];                                                                             \
+    uint32_t s_raw[4], b_raw[4];                                                                         \
+    _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                                   \
+      read_codes(t, 16 * ct + r, words[ct]);                                                             \
+      ws.params(t, 16 * ct + r, 0, &s_raw[ct], &b_raw[ct]);                                              \
+    }                                                                                                    \
+    wait_lds_reads();                                                                                    \
+    issue_all((J), min(t + 4, last & ~3), min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)),           \
+              min(t + 3, last));                                                                         \
+    f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, ones, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0); \
+    xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, ones, xs, 0, 0, 0);                                 \
+    _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                                   \
+      u32x4_t op[2];                                                                                     \
+      codes_bf16<BITS>(words[ct], op);                                                                   \
+      f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, __builtin_bit_cast(bf16x8_t, op[0]),       \
+                                                          f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);     \
+      q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, __builtin_bit_cast(bf16x8_t, op[1]), q, 0, 0, 0);  \
+      const float sv = widen_param<PT>(s_raw[ct]) * code_scale, bv = widen_param<PT>(b_raw[ct]);         \
+      _Pragma("unroll") for (int i = 0; i < 4; ++i) y[ct][i] = fmaf(sv, q[i], fmaf(bv, xs[i], y[ct][i])); \
+    }                                                                                                    \
+    ++t;                                                                                                 \
+  }
+
+  for (int t = 0; t < steps;) {
+    AFFON_QSKINNY_STEP(0)
+    AFFON_QSKINNY_STEP(1)
+    AFFON_QSKINNY_STEP(2)
+    AFFON_QSKINNY_STEP(3)
+  }
+#undef AFFON_QSKINNY_STEP
+  wait_vmcnt<0>();  // no transfer in flight at exit
+
+  // Output element i of column tile ct: row 4h + i, column n0 + 16ct + r.
+  float* dst = a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const int col = n0 + 16 * ct + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * h + i;
+      if (row < a.M && col < a.N) dst[static_cast<int64_t>(row) * a.N + col] = y[ct][i];
+    }
+  }
+}
+
+template <int BITS, typename PT>
+hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
+  const int tiles = (args.N + kCols - 1) / kCols;
+  hipLaunchKernelGGL((qskinny_kernel<BITS, PT>), dim3(tiles * args.splits), dim3(kThreads), 0, stream, args);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || args.splits == 1) return e;
+  return launch_reduce(args, stream);
+}
+
+}  // namespace
+
+bool gemv_mfma_supports(const QmmProblem& p) {
+  if (p.x_dtype != AFFON_ROCM_BF16 || p.M > kRows) return false;
+  if (p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
+  // Each K step inside one group, groups addressed by shift.
+  if (p.K % (4 * kBK) != 0 || p.group % kBK != 0) return false;
+  const int64_t gq = p.group / 32;
+  if ((gq & (gq - 1)) != 0) return false;
+  if (reinterpret_cast<uintptr_t>(p.x) % 16 != 0 || (p.xs0 * 2) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0 || p.ws0 % 4 != 0) return false;
+  const int64_t pbytes = p.p_dtype == AFFON_ROCM_BF16 ? 2 : 4;
+  if (reinterpret_cast<uintptr_t>(p.s) % 4 != 0 || reinterpret_cast<uintptr_t>(p.b) % 4 != 0) return false;
+  if ((p.ss0 * pbytes) % 4 != 0 || (p.bs0 * pbytes) % 4 != 0 || (p.K / p.group * pbytes) % 4 != 0) return false;
+  if (p.N > (int64_t(1) << 30) || p.K > (int64_t(1) << 30)) return false;
+  return true;
+}
+
+hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
+  TileArgs a;
+  a.x = reinterpret_cast<const uint16_t*>(p.x);
+  a.xs0 = p.xs0;
+  a.w = p.w;
+  a.ws0 = p.ws0;
+  a.s = p.s;
+  a.ss0 = p.ss0;
+  a.b = p.b;
+  a.bs0 = p.bs0;
+  a.out = p.out;
+  a.M = static_cast<int>(p.M);
+  a.N = static_cast<int>(p.N);
+  a.K = static_cast<int>(p.K);
+  a.group_shift = 0;
+  while ((int64_t(32) << a.group_shift) < p.group) ++a.group_shift;
+  const int tiles = static_cast<int>((p.N + kCols - 1) / kCols);
+  const int steps = static_cast<int>(p.K / kBK);
+  a.splits = 1;
+  a.split_steps = steps;
+  a.partial = nullptr;
+  const int splits = l.workspace != nullptr ? choose_splits(tiles, steps) : 1;
+  if (splits > 1) {
+    if (auto* w = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * p.N * 4))) {
+      a.splits = splits;
+      a.split_steps = steps / splits;
+      a.partial = w;
+    }
+  }
+  const bool bf16p = p.p_dtype == AFFON_ROCM_BF16;
+  switch (p.bits) {
+    case 2: return bf16p ? launch_typed<2, BF16>(a, l.stream) : launch_typed<2, F32>(a, l.stream);
+    case 4: return bf16p ? launch_typed<4, BF16>(a, l.stream) : launch_typed<4, F32>(a, l.stream);
+    default: return bf16p ? launch_typed<8, BF16>(a, l.stream) : launch_typed<8, F32>(a, l.stream);
+  }
+}
+
+}  // namespace affon

@@ -1,0 +1,282 @@
+// Shared pieces of the tiled quantized-matmul kernels (prefill GEMM and the
+// small-M MFMA decode kernel) for gfx950: direct global-to-LDS transfers with
+// counted waits, the packed-word / parameter transfer plan of one wave, the
+// split of K over workgroups and the ordered reduction of its partial sums.
+#pragma once
+
+#include <mutex>
+#include <type_traits>
+
+#include "device.h"
+#include "internal.h"
+
+namespace affon {
+namespace pipeline {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBK = 64;        // K step
+constexpr int kWaves = 4;      // waves per workgroup, side by side along N (64 columns each)
+constexpr int kThreads = 64 * kWaves;
+constexpr int kStages = 4;     // LDS ring depth (steps)
+
+// Operands of one tiled launch.
+struct TileArgs {
+  const uint16_t* x;  // bf16 [M, K], row stride xs0 elements
+  int64_t xs0;
+  const uint32_t* w;  // packed [N, K/P], row stride ws0 words
+  int64_t ws0;
+  const uint8_t* s;
+  int64_t ss0;
+  const uint8_t* b;
+  int64_t bs0;
+  float* out;  // [M, N]
+  int M, N, K;
+  int group_shift;  // log2(group / 32): groups of 32, 64, 128, ...
+  // Split of K over workgroups: splits ranges of split_steps K steps each.
+  // With splits > 1 each range writes its sums to partial [splits, M, N] f32
+  // and reduce_partials_kernel forms the output.
+  int splits, split_steps;
+  float* partial;
+};
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{static_cast<__bf16>(a), static_cast<__bf16>(b)});
+}
+
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Waits until at most N vector-memory operations of this wave are in flight.
+// Written as asm with a memory clobber so that no memory access moves across
+// it (the compiler does not see the direct-to-LDS loads it stands guard for).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Waits until this wave's LDS reads have returned (memory clobber: no memory
+// access moves across it), e.g. before a transfer may overwrite what they read.
+__device__ __forceinline__ void wait_lds_reads() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// size bytes per lane (4 or 16) from global memory straight into LDS: lane
+// L's bytes land at lds_addr + size * L (lds_addr wave-uniform). Issued as
+// asm: the compiler would otherwise drain the load counter before every LDS
+// read it cannot prove disjoint from the transfer; here the caller orders them
+// with wait_vmcnt and a barrier.
+template <int SIZE>
+__device__ __forceinline__ void load_lds(const void* src, uint32_t lds_addr) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  if constexpr (SIZE == 16)
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// Compile-time unrolled loop: f(std::integral_constant<int, I>) for I in [I0, N).
+template <int I, int N>
+struct Unroll {
+  template <class F>
+  __device__ __forceinline__ static void run(F&& f) {
+    f(std::integral_constant<int, I>{});
+    Unroll<I + 1, N>::run(f);
+  }
+};
+template <int N>
+struct Unroll<N, N> {
+  template <class F>
+  __device__ __forceinline__ static void run(F&&) {}
+};
+
+// Transfer plan of one wave (64 weight columns) for a weight format, with
+// ALOADS activation transfer instructions per step and wave.
+//
+// Packed words reach LDS in runs of kColBytes per column: four K steps at a
+// time for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per column), one step at a
+// time for 8-bit (64 bytes) -- so each transfer instruction covers whole
+// half or full 128-byte lines. Inside a column run the 16-byte slots are
+// XOR-swizzled with the column index so that the decode's fragment reads
+// (lanes = consecutive columns) are bank-conflict free whether the LDS serves
+// 8 lanes x 16 bytes (128 bytes) or 16 lanes x 16 bytes (256 bytes) per cycle. Scales and biases come as one 16-byte window per
+// column every four steps (four lanes per column, one dword each; bf16: 8
+// groups, f32: 4 groups), starting at the dword that holds the first group of
+// those 256 k values, which covers all of their groups for the group sizes
+// the kernel accepts; dwords past the row end repeat the row's last dword.
+template <int BITS, typename PT, int ALOADS>
+struct Plan {
+  static constexpr int kStepsPerW = BITS == 8 ? 1 : 4;           // steps per packed-word transfer
+  static constexpr int kColBytes = 8 * BITS * kStepsPerW;         // bytes per column per transfer
+  static constexpr int kSlots = kColBytes / 16;                   // 16-byte slots per column run
+  static constexpr int kWLoads = 64 * kColBytes / 1024;           // 16-byte DMA instructions per transfer
+  static constexpr int kWBytes = 64 * kColBytes;                  // per wave and buffer
+  static constexpr int kWBufs = kStepsPerW == 1 ? kStages : 2;    // ring depth (buffers)
+  static constexpr int kPLoads = 8;                               // 4-byte DMA: 4 for scales, 4 for biases
+  static constexpr int kPBytes = 2 * 64 * 16;                     // per wave and buffer: 16-byte windows of scales, biases
+  static constexpr int kALoads = ALOADS;                          // activation DMA instructions per step
+
+  // Slot (16-byte unit) holding part `part` of column c's run. 128-byte runs:
+  // within 8 consecutive columns the slots differ; columns c and c+8 (same
+  // 128-byte bank phase in a 256-byte window) differ in slot bit 0. 64-byte
+  // runs: even columns 0,2,4,6 (and odd 1,3,5,7) use different slots, and so
+  // do columns c, c+4, c+8, c+12.
+  static __device__ __forceinline__ int slot(int c, int part) {
+    return kSlots == 8 ? part ^ (c & 7) ^ ((c >> 3) & 1) : part ^ (((c >> 1) ^ (c >> 3)) & 3);
+  }
+
+  // Transfers issued by iteration j (= step index mod 4), in issue order
+  // parameters, words, activations; group 0 = parameters, 1 = words, 2 = activations.
+  static constexpr int group_ops(int j, int g) {
+    return g == 0 ? (j == 0 ? kPLoads : 0) : g == 1 ? (kStepsPerW == 1 || j == 0 ? kWLoads : 0) : kALoads;
+  }
+  static constexpr int ops(int j) { return group_ops(j, 0) + group_ops(j, 1) + group_ops(j, 2); }
+  // Transfers issued after group g of the iteration r iterations before one
+  // with index j, up to the start of that one.
+  static constexpr int ops_after(int j, int r, int g) {
+    const int jr = ((j - r) % 4 + 4) % 4;
+    int n = 0;
+    for (int h = g + 1; h < 3; ++h) n += group_ops(jr, h);
+    for (int i = 1; i < r; ++i) n += ops(((j - i) % 4 + 4) % 4);
+    return n;
+  }
+  // vmcnt bound at the start of iteration j: the activations of its step
+  // (issued three iterations before) and the words and parameters of the
+  // next step (decoded during it) must have landed.
+  static constexpr int wait(int j) {
+    int n = ops_after(j, 3, 2);
+    const int rw = kStepsPerW == 1 ? 3 : (j == 3 ? 3 : j + 4);
+    const int rp = j == 3 ? 3 : j + 4;
+    const int nw = ops_after(j, rw, 1), np = ops_after(j, rp, 0);
+    n = nw < n ? nw : n;
+    n = np < n ? np : n;
+    return n;
+  }
+  static_assert(kWLoads * 1024 == kWBytes, "whole DMA instructions");
+};
+
+// The packed-word and parameter transfers of one wave's 64 columns
+// [n0, n0 + 64) over one K range starting at global step s0, per Plan, into
+// the wave's slices of a ring of LDS buffers: w_lds(buf) = w_base + buf *
+// w_stride (Plan::kWBufs buffers of kWBytes), p_lds(buf) likewise (2 buffers
+// of kPBytes). Steps passed to the methods are local to the K range.
+template <int BITS, typename PT, int ALOADS>
+struct WeightStream {
+  using P = Plan<BITS, PT, ALOADS>;
+  const uint8_t* w_src[P::kWLoads];
+  const uint8_t* s_col[4];
+  const uint8_t* b_col[4];
+  uint8_t* w_base;
+  uint8_t* p_base;
+  int w_stride, p_stride;
+  int s0, group_shift, row_dwords, lane;
+
+  __device__ __forceinline__ void init(const TileArgs& a, int n0, int s0_, int lane_, uint8_t* w_base_, int w_stride_,
+                                       uint8_t* p_base_, int p_stride_) {
+    s0 = s0_;
+    lane = lane_;
+    group_shift = a.group_shift;
+    w_base = w_base_;
+    w_stride = w_stride_;
+    p_base = p_base_;
+    p_stride = p_stride_;
+    // Packed-word transfers: DMA lane L of instruction j writes LDS byte
+    // 1024j + 16L of the buffer = slot (16L % kColBytes) / 16 of local column
+    // (1024j + 16L) / kColBytes, which holds part slot ^ swizzle.
+#pragma unroll
+    for (int j = 0; j < P::kWLoads; ++j) {
+      const int pos = 1024 * j + 16 * lane;
+      const int c = pos / P::kColBytes;
+      const int part = P::slot(c, (pos % P::kColBytes) / 16);  // the swizzle is an involution
+      const int col = min(n0 + c, a.N - 1);  // columns past N feed unstored outputs
+      w_src[j] = reinterpret_cast<const uint8_t*>(a.w + static_cast<int64_t>(col) * a.ws0) + 16 * part;
+    }
+    // Parameter windows: DMA lane L of instruction i carries dword L%4 of the
+    // window of local column 16i + L/4, stored at byte 16*(16i + L/4) + 4*(L%4).
+    row_dwords = (a.K >> (5 + a.group_shift)) * PT::bytes / 4;  // whole dwords per parameter row
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = min(n0 + 16 * i + (lane >> 2), a.N - 1);
+      s_col[i] = a.s + static_cast<int64_t>(col) * a.ss0 * PT::bytes;
+      b_col[i] = a.b + static_cast<int64_t>(col) * a.bs0 * PT::bytes;
+    }
+  }
+  // First dword of the parameter window for the four global steps starting at gstep.
+  __device__ __forceinline__ int window(int gstep) const {
+    return (((gstep * kBK) >> (5 + group_shift)) * PT::bytes) >> 2;
+  }
+  __device__ __forceinline__ int w_buf(int step) const { return P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1); }
+  __device__ __forceinline__ const uint8_t* w_lds(int step) const { return w_base + w_buf(step) * w_stride; }
+  __device__ __forceinline__ const uint8_t* p_lds(int step) const { return p_base + ((step >> 2) & 1) * p_stride; }
+  // Parameter window instruction i (0..3 scales, 4..7 biases) of the four
+  // steps starting at `step` (a multiple of 4).
+  __device__ __forceinline__ void issue_p(int step, int i) const {
+    const uint32_t dst = lds_address(p_lds(step)) + (i < 4 ? 256 * i : 1024 + 256 * (i - 4));
+    const int off = 4 * min(window(s0 + step) + (lane & 3), row_dwords - 1);
+    load_lds<4>((i < 4 ? s_col[i] : b_col[i - 4]) + off, dst);
+  }
+  // Packed-word instruction j of the transfer starting at `step`.
+  __device__ __forceinline__ void issue_w(int step, int j) const {
+    load_lds<16>(w_src[j] + static_cast<int64_t>(s0 + step) * (8 * BITS), lds_address(w_lds(step)) + 1024 * j);
+  }
+  // Bytes [off, off + n) of local column c's packed run for `step`, as laid
+  // out by the swizzle: 16-byte part q of the step's BITS*8 bytes.
+  __device__ __forceinline__ const uint8_t* w_part(int step, int c, int q) const {
+    const int sub = P::kStepsPerW == 1 ? 0 : (step & 3);  // step within the transfer
+    return w_lds(step) + c * P::kColBytes + 16 * P::slot(c, sub * (BITS / 2) + q);
+  }
+  // Raw scale and bias bits (bf16 in the low half, or f32) of local column c
+  // for the group holding k offset `k` of `step`.
+  __device__ __forceinline__ void params(int step, int c, int k, uint32_t* s_raw, uint32_t* b_raw) const {
+    const int g = (((s0 + step) * kBK + k) >> (5 + group_shift)) - window(s0 + (step & ~3)) * (4 / PT::bytes);
+    const uint8_t* pbuf = p_lds(step);
+    if constexpr (PT::bytes == 2) {
+      *s_raw = *reinterpret_cast<const uint16_t*>(pbuf + 16 * c + 2 * g);
+      *b_raw = *reinterpret_cast<const uint16_t*>(pbuf + 1024 + 16 * c + 2 * g);
+    } else {
+      *s_raw = *reinterpret_cast<const uint32_t*>(pbuf + 16 * c + 4 * g);
+      *b_raw = *reinterpret_cast<const uint32_t*>(pbuf + 1024 + 16 * c + 4 * g);
+    }
+  }
+};
+
+template <typename PT>
+__device__ __forceinline__ float widen_param(uint32_t raw) {
+  return PT::bytes == 2 ? __uint_as_float(raw << 16) : __uint_as_float(raw);
+}
+
+// Work unit (tile, K range) of this workgroup: consecutive blocks go to
+// consecutive XCDs, so the block index is remapped to give each XCD a
+// contiguous run of units (same K range, neighbouring tiles).
+__device__ __forceinline__ void work_unit(int tiles, int splits, int* tile, int* split) {
+  const int units = tiles * splits;
+  int unit = blockIdx.x;
+  if ((units & 7) == 0) unit = (unit & 7) * (units >> 3) + (unit >> 3);
+  *split = unit / tiles;
+  *tile = unit % tiles;
+}
+
+int device_cus();
+
+// Number of K ranges: 1 when the tiles alone fill three quarters of the CUs;
+// otherwise the smallest count of equal 4-step-aligned ranges (at most 8, at
+// least 8 steps each) that does, or the largest allowed.
+int choose_splits(int tiles, int steps);
+
+// Enqueues the ordered sum of args.splits partial planes into args.out.
+hipError_t launch_reduce(const TileArgs& args, hipStream_t stream);
+
+}  // namespace pipeline
+}  // namespace affon

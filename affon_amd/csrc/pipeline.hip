@@ -1,0 +1,69 @@
+// Host-side pieces shared by the tiled kernels, and the ordered reduction of
+// split-K partial sums.
+#include "lds_pipeline.h"
+
+namespace affon {
+namespace pipeline {
+namespace {
+
+// out[i] = sum of the K ranges' partial sums, added in range order (the same
+// result on every run). Four outputs per thread; `count` = M*N; `vec` when
+// count % 4 == 0 and out is 16-byte aligned (partial always is).
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* partial, float* out, int64_t count,
+                                                              int splits, int vec) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= count) return;
+  if (vec) {
+    f32x4_t sum = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + i));
+    for (int r = 1; r < splits; ++r) sum += __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + r * count + i));
+    *reinterpret_cast<f32x4_t*>(out + i) = sum;
+  } else {
+    for (int64_t j = i; j < i + 4 && j < count; ++j) {
+      float sum = partial[j];
+      for (int r = 1; r < splits; ++r) sum += partial[r * count + j];
+      out[j] = sum;
+    }
+  }
+}
+
+}  // namespace
+
+int device_cus() {
+  static std::mutex mutex;
+  static int cached[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mutex);
+  if (cached[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
+    cached[device] = cus;
+  }
+  return cached[device];
+}
+
+int choose_splits(int tiles, int steps) {
+  const int target = device_cus() * 3 / 4;
+  int splits = 1;
+  if (tiles >= target) return 1;
+  for (int s = 2; s <= 8; ++s) {
+    if ((steps / 4) % s != 0) continue;
+    if (steps / s < 8) break;
+    splits = s;
+    if (tiles * s >= target) break;
+  }
+  return splits;
+}
+
+
+hipError_t launch_reduce(const TileArgs& args, hipStream_t stream) {
+  const int64_t count = static_cast<int64_t>(args.M) * args.N;
+  const int64_t blocks = (count + 1023) / 1024;
+  const int vec = count % 4 == 0 && reinterpret_cast<uintptr_t>(args.out) % 16 == 0;
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                     args.partial, args.out, count, args.splits, vec);
+  return hipGetLastError();
+}
+
+}  // namespace pipeline
+}  // namespace affon

@@ -389,6 +389,37 @@ def test_prefill_seeded_against_oracle(session, bits, group):
         check_against_oracle(run_mfma(session, xt, wt, st, bt, bits, group), x, packed, s, b, bits, group, True)
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("p_dtype", ["bf16", "f32"])
+def test_gemv_mfma_exact_integer_products(session, bits, p_dtype, rng):
+    """Small-M MFMA decode kernel: integer codes times integer activations with
+    power-of-two scales and integer biases keep every step sum exact, so the
+    output must equal the f64 reference exactly (partial column tiles, one or
+    many K steps, split K)."""
+    for M, N, K, group in [(1, 40, 256, 64), (2, 300, 1024, 128), (5, 129, 4096, 64), (16, 1000, 2048, 256),
+                           (16, 4096, 14336, 64)]:
+        q = rng.integers(0, 1 << bits, size=(N, K))
+        x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
+        s = 2.0 ** rng.integers(-3, 1, size=(N, K // group))
+        b = rng.integers(-2, 3, size=(N, K // group)).astype(np.float64)
+        expected = reference_f64(x, q, s, b, group)
+        xt = upload(session, storage(x, "bf16"), "bf16")
+        wt = upload(session, pack_codes(q, bits), "u32")
+        st, bt = upload(session, storage(s, p_dtype), p_dtype), upload(session, storage(b, p_dtype), p_dtype)
+        out = session.empty("f32", (M, N))
+        A.quantized_matmul_into(out, xt, wt, st, bt, bits=bits, group_size=group, implementation="gemv_mfma")
+        np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
+
+
+def test_gemv_mfma_selected_for_decode_batches(session):
+    x, packed, s, b = seeded_problem(8, 512, 1024, 4, 64, "bf16", "bf16")
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=64) == "rocm_quantized_matmul.gemv_mfma"
+    x, packed, s, b = seeded_problem(1, 512, 1024, 4, 64, "bf16", "bf16")
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=64) == "rocm_quantized_matmul.gemv"
+
+
 def test_prefill_split_k_deterministic(session):
     """Shapes with few tiles split K over workgroups (partials summed in range
     order by the last arrival): repeated runs are bit-identical, and match the
