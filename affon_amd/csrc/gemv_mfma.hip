@@ -1,4 +1,4 @@
-// rocm_quantized_matmul.gemv_mfma — decode batches (M <= 16) with bf16
+// rocm_quantized_matmul.gemv_mfma — decode batches (M <= 32) with bf16
 // activations on the matrix cores.
 //
 // Counterpart of the reference's small-M decode variants (metal simd4 /
@@ -10,11 +10,11 @@
 // step sums: y += s * sum(x*q) + b * sum(x) -- the arithmetic of the VALU
 // decode kernel, with sum(x) from one more MFMA against a bf16 ones operand.
 //
-// Work mapping: a 16 x 256 tile per workgroup (rows past M repeat row M-1
-// and are not stored), four waves side by side along N with 4 MFMA column
-// tiles of 16 each, K split over workgroups when the tiles alone cannot fill
-// the GPU. Operands reach LDS by the same direct transfers, ring and counted
-// waits as the prefill GEMM (lds_pipeline.h).
+// Work mapping: a (16 or 32) x 64 tile per workgroup (rows past M repeat row
+// M-1 and are not stored), its four waves each on a quarter of the K range, K
+// split further over workgroups when the tiles alone cannot fill the GPU.
+// Operands reach LDS by the same direct transfers, ring and counted waits as
+// the prefill GEMM (lds_pipeline.h).
 
 #include "lds_pipeline.h"
 
@@ -23,10 +23,8 @@ namespace {
 
 using namespace pipeline;
 
-constexpr int kRows = 16;                        // activation rows per tile
-constexpr int kCols = 256;                       // weight columns per tile
-constexpr int kXStageBytes = kRows * kBK * 2;    // 2 KiB: 16 rows x 128 bytes
-constexpr int kXLoads = 1;                       // activation DMA instructions per wave and step
+constexpr int kMaxRows = 32;  // activation rows per tile: up to two blocks of 16 MFMA rows
+constexpr int kCols = 64;     // weight columns per workgroup (4 MFMA column tiles)
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -86,42 +84,67 @@ __device__ __forceinline__ void codes_bf16(const uint32_t* words, u32x4_t* op) {
   }
 }
 
-// Workgroup tile 16 x 256, K step 64 (one group or part of one), four waves
-// side by side along N, each 16 rows x 64 columns = 4 column tiles.
+// Workgroup: 64 weight columns (4 MFMA column tiles of 16) x up to 32
+// activation rows (XROWS = 8, 16 or 32 staged; 32 rows run as two blocks of
+// 16 MFMA rows sharing the decoded codes); its four waves split the
+// workgroup's K range into four contiguous parts of whole 4-step chunks and
+// run independently (no barrier inside the K loop), each with its own
+// activation transfers. At the end the four partial sums are added in wave
+// order through LDS (each wave's activation ring, free by then).
 //
 // K order inside a step: MFMA t of lane quarter h (lanes 16h .. 16h+15)
 // covers k = 16h + 8t .. 16h + 8t + 7, for both operands, so a lane's codes
 // for the step are one contiguous run of 16 and every MFMA stays inside the
-// step. The 16 activation rows of a step sit in LDS as 16-byte chunks, chunk
-// c of row r at slot c ^ (r%8) ^ ((r/8)%2) (conflict-free fragment reads);
-// wave w transfers rows 4w .. 4w+3 (one DMA instruction, lanes 0..31).
-template <int BITS, typename PT>
+// step. A wave's XROWS activation rows of a step sit in LDS as 16-byte
+// chunks, chunk c of row r at slot c ^ (r%8) ^ ((r/8)%2) (conflict-free
+// fragment reads); with XROWS = 8 the MFMA rows 8..15 repeat rows 0..7 and
+// are not stored.
+template <int XROWS>
+struct RowBlocks {
+  static constexpr int kBlocks = XROWS > 16 ? 2 : 1;  // blocks of 16 MFMA rows
+  static constexpr int kRows = 16 * kBlocks;           // rows with results
+};
+template <int BITS, typename PT, int XROWS>
 __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
+  constexpr int kXLoads = XROWS / 8;  // activation DMA instructions per step
   using P = Plan<BITS, PT, kXLoads>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_x[kStages][kXStageBytes];
+  constexpr int RB = RowBlocks<XROWS>::kBlocks;
+  constexpr int kRows = RowBlocks<XROWS>::kRows;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_x[kWaves][kStages][XROWS * 128];
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[P::kWBufs][kWaves][P::kWBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_p[2][kWaves][P::kPBytes];
+  static_assert(kRows * kCols * 4 <= kStages * XROWS * 128, "partial sums fit in a wave's activation ring");
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int r = lane & 15;   // row of the A operand and column of the B operand and output
+  const int r = lane & 15;   // row of the A operand, column of the B operand and output
   const int h = lane >> 4;   // lane quarter
 
   const int nb_n = (a.N + kCols - 1) / kCols;
   int tile, split;
   work_unit(nb_n, a.splits, &tile, &split);
-  const int n0 = tile * kCols + 64 * wave;  // this wave's first column
-  const int steps = a.split_steps;
-  const int s0 = split * steps;
+  const int n0 = tile * kCols;
+  // K range of this wave, in whole 4-step chunks: chunks [c0, c1) of the
+  // workgroup's range, itself chunks [split*C/S, (split+1)*C/S) of K.
+  const int chunks = a.K / (4 * kBK);
+  const int g0 = split * chunks / a.splits, g1 = (split + 1) * chunks / a.splits;
+  const int c0 = g0 + wave * (g1 - g0) / kWaves, c1 = g0 + (wave + 1) * (g1 - g0) / kWaves;
+  const int steps = 4 * (c1 - c0);
+  const int s0 = 4 * c0;
   const int last = steps - 1;
 
-  // Activation transfer: lane L < 32 writes slot L%8 of row 4w + L/8.
-  const int xrow = 4 * wave + ((lane >> 3) & 3);
-  const uint16_t* x_src = a.x + static_cast<int64_t>(min(xrow, a.M - 1)) * a.xs0 +
-                          8 * ((lane & 7) ^ (xrow & 7) ^ ((xrow >> 3) & 1));
-  auto issue_a = [&](int step, int) {
-    if (lane < 32) load_lds<16>(x_src + (s0 + step) * kBK, lds_address(lds_x[step & 3]) + 512 * wave);
+  // Activation transfer i: lane L writes slot L%8 of row 8i + L/8.
+  const uint16_t* x_src[kXLoads];
+#pragma unroll
+  for (int i = 0; i < kXLoads; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    x_src[i] = a.x + static_cast<int64_t>(min(row, a.M - 1)) * a.xs0 + 8 * ((lane & 7) ^ (row & 7) ^ ((row >> 3) & 1));
+  }
+  auto issue_a = [&](int step) {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i)
+      load_lds<16>(x_src[i] + (s0 + step) * kBK, lds_address(lds_x[wave][step & 3]) + 1024 * i);
   };
   WeightStream<BITS, PT, kXLoads> ws;
   ws.init(a, n0, s0, lane, lds_w[0][wave], kWaves * P::kWBytes, lds_p[0][wave], kWaves * P::kPBytes);
@@ -130,12 +153,14 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
       for (int i = 0; i < P::kPLoads; ++i) ws.issue_p(pstep, i);
     if (P::kStepsPerW == 1 || j == 0)
       for (int i = 0; i < P::kWLoads; ++i) ws.issue_w(wstep, i);
-    issue_a(astep, 0);
+    issue_a(astep);
   };
-  // A operand of MFMA t: row r, chunk 2h + t.
-  auto read_x = [&](int stage, int t) -> bf16x8_t {
-    const int slot = (2 * h + t) ^ (r & 7) ^ ((r >> 3) & 1);
-    return *reinterpret_cast<const bf16x8_t*>(&lds_x[stage][(r >> 3) * 1024 + (8 * (r & 7) + slot) * 16]);
+  // A operand of MFMA t for row block rb: row 16rb + r (taken mod XROWS when
+  // only 8 rows are staged), chunk 2h + t.
+  auto read_x = [&](int stage, int rb, int t) -> bf16x8_t {
+    const int row = (16 * rb + r) % XROWS;
+    const int slot = (2 * h + t) ^ (row & 7) ^ ((row >> 3) & 1);
+    return *reinterpret_cast<const bf16x8_t*>(&lds_x[wave][stage][(row >> 3) * 1024 + (8 * (row & 7) + slot) * 16]);
   };
   // The lane's 16 codes of column c (local) for `step`.
   auto read_codes = [&](int step, int c, uint32_t* words) {
@@ -156,24 +181,26 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
 
   const float code_scale = BITS == 8 ? 1.0f : 512.0f;
   const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
-  f32x4_t y[4];
+  f32x4_t y[RB][4];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) y[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Transfers exactly as the prefill GEMM orders them (Plan<..., kXLoads>):
-  // iterations -4 .. -1 issue the prologue, iteration t issues parameters and
-  // words at t%4 == 0 (2/4-bit) or every step (8-bit words), then the
-  // activations of step t+3. Step t is decoded in iteration t from LDS reads
-  // that complete before that iteration's transfers are issued: the 8-bit
-  // words of step t+4 reuse step t's buffer.
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) issue_all(rr, 0, min(rr, last), min(max(rr - 1, 0), last));
+    for (int ct = 0; ct < 4; ++ct) y[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // Transfers exactly as the prefill GEMM orders them (Plan<..., kXLoads>),
+  // but each wave for itself: iterations -4 .. -1 issue the prologue,
+  // iteration t issues parameters and words at t%4 == 0 (2/4-bit) or every
+  // step (8-bit words), then the activations of step t+3. Step t is decoded
+  // in iteration t from LDS reads that complete before that iteration's
+  // transfers are issued: the 8-bit words of step t+4 reuse step t's buffer.
 #define AFFON_QSKINNY_STEP(J)                                                                            \
   {                                                                                                      \
     wait_vmcnt<P::wait(J)>();                                                                            \
-    __syncthreads();                                                                                     \
-    const bf16x8_t x0 = read_x((J), 0), x1 = read_x((J), 1);                                             \
+    bf16x8_t xf[RB][2];                                                                                  \
+    _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                  \
+      xf[rb][0] = read_x((J), rb, 0);                                                                    \
+      xf[rb][1] = read_x((J), rb, 1);                                                                    \
+    }                                                                                                    \
     uint32_t words[4][BITS];                                                                             \
     uint32_t s_raw[4], b_raw[4];                                                                         \
     _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                                   \
@@ -183,38 +210,59 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
     wait_lds_reads();                                                                                    \
     issue_all((J), min(t + 4, last & ~3), min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)),           \
               min(t + 3, last));                                                                         \
-    f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, ones, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0); \
-    xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, ones, xs, 0, 0, 0);                                 \
+    f32x4_t xs[RB];                                                                                      \
+    _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                  \
+      xs[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][0], ones, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0); \
+      xs[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][1], ones, xs[rb], 0, 0, 0);                \
+    }                                                                                                    \
     _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                                   \
       u32x4_t op[2];                                                                                     \
       codes_bf16<BITS>(words[ct], op);                                                                   \
-      f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, __builtin_bit_cast(bf16x8_t, op[0]),       \
-                                                          f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);     \
-      q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, __builtin_bit_cast(bf16x8_t, op[1]), q, 0, 0, 0);  \
       const float sv = widen_param<PT>(s_raw[ct]) * code_scale, bv = widen_param<PT>(b_raw[ct]);         \
-      _Pragma("unroll") for (int i = 0; i < 4; ++i) y[ct][i] = fmaf(sv, q[i], fmaf(bv, xs[i], y[ct][i])); \
+      _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                \
+        f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][0], __builtin_bit_cast(bf16x8_t, op[0]), \
+                                                            f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);   \
+        q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][1], __builtin_bit_cast(bf16x8_t, op[1]), q, 0, 0, 0); \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                    \
+            y[rb][ct][i] = fmaf(sv, q[i], fmaf(bv, xs[rb][i], y[rb][ct][i]));                            \
+      }                                                                                                  \
     }                                                                                                    \
     ++t;                                                                                                 \
   }
 
-  for (int t = 0; t < steps;) {
-    AFFON_QSKINNY_STEP(0)
-    AFFON_QSKINNY_STEP(1)
-    AFFON_QSKINNY_STEP(2)
-    AFFON_QSKINNY_STEP(3)
+  if (steps > 0) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) issue_all(rr, 0, min(rr, last), min(max(rr - 1, 0), last));
+    for (int t = 0; t < steps;) {
+      AFFON_QSKINNY_STEP(0)
+      AFFON_QSKINNY_STEP(1)
+      AFFON_QSKINNY_STEP(2)
+      AFFON_QSKINNY_STEP(3)
+    }
+    wait_vmcnt<0>();  // no transfer in flight past this point
   }
 #undef AFFON_QSKINNY_STEP
-  wait_vmcnt<0>();  // no transfer in flight at exit
 
-  // Output element i of column tile ct: row 4h + i, column n0 + 16ct + r.
+  // Partial sums of the four K parts, [kRows][kCols] f32 per wave in the
+  // wave's own activation ring (no transfer into it is in flight any more):
+  // output element i of row block rb and column tile ct is row 16rb + 4h + i,
+  // column 16ct + r. Added in wave order.
+  auto ysum = [&](int w) { return reinterpret_cast<float*>(&lds_x[w][0][0]); };
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ysum(wave)[(16 * rb + 4 * h + i) * kCols + 16 * ct + r] = y[rb][ct][i];
+  __syncthreads();
   float* dst = a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N;
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int col = n0 + 16 * ct + r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * h + i;
-      if (row < a.M && col < a.N) dst[static_cast<int64_t>(row) * a.N + col] = y[ct][i];
+  for (int e = 0; e < kRows * kCols / kThreads; ++e) {
+    const int o = e * kThreads + tid;
+    const int row = o / kCols, col = n0 + o % kCols;
+    if (row < a.M && col < a.N) {
+      const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
+      dst[static_cast<int64_t>(row) * a.N + col] = v;
     }
   }
 }
@@ -222,7 +270,13 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
 template <int BITS, typename PT>
 hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
   const int tiles = (args.N + kCols - 1) / kCols;
-  hipLaunchKernelGGL((qskinny_kernel<BITS, PT>), dim3(tiles * args.splits), dim3(kThreads), 0, stream, args);
+  const dim3 grid(tiles * args.splits);
+  if (args.M <= 8)
+    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 8>), grid, dim3(kThreads), 0, stream, args);
+  else if (args.M <= 16)
+    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 16>), grid, dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 32>), grid, dim3(kThreads), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || args.splits == 1) return e;
   return launch_reduce(args, stream);
@@ -231,7 +285,7 @@ hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
 }  // namespace
 
 bool gemv_mfma_supports(const QmmProblem& p) {
-  if (p.x_dtype != AFFON_ROCM_BF16 || p.M > kRows) return false;
+  if (p.x_dtype != AFFON_ROCM_BF16 || p.M > kMaxRows) return false;
   if (p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
   // Each K step inside one group, groups addressed by shift.
   if (p.K % (4 * kBK) != 0 || p.group % kBK != 0) return false;
@@ -263,15 +317,18 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
   a.group_shift = 0;
   while ((int64_t(32) << a.group_shift) < p.group) ++a.group_shift;
   const int tiles = static_cast<int>((p.N + kCols - 1) / kCols);
-  const int steps = static_cast<int>(p.K / kBK);
+  const int chunks = static_cast<int>(p.K / (4 * kBK));
   a.splits = 1;
-  a.split_steps = steps;
+  a.split_steps = 0;  // ranges are computed per workgroup from K and splits
   a.partial = nullptr;
-  const int splits = l.workspace != nullptr ? choose_splits(tiles, steps) : 1;
+  // Further K ranges over workgroups while the tiles fill less than three
+  // quarters of the CUs and every wave keeps at least two chunks.
+  int splits = 1;
+  if (l.workspace != nullptr)
+    while (splits < 8 && tiles * splits < device_cus() * 3 / 4 && chunks >= 2 * kWaves * 2 * splits) splits *= 2;
   if (splits > 1) {
     if (auto* w = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * p.N * 4))) {
       a.splits = splits;
-      a.split_steps = steps / splits;
       a.partial = w;
     }
   }

@@ -210,6 +210,67 @@ def load_traffic(name: str):
     return None if entry is None else entry["traffic_bytes"]
 
 
+LLAMA8B_LAYER = (("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+                 ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336), ("lm_head", 128256, 4096))
+
+
+def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int) -> dict:
+    """The Llama-8B-shaped projections at 4-bit group 64 (bf16 x, scales and
+    biases; one weight seed per projection), run back to back on one stream:
+    a step is the whole sequence. Weights total 4.4 GB per set, larger than
+    the MALL, so no rotation is needed."""
+    import affon_amd as A
+    from affon_amd import ops
+    lib = ops._native.load()
+    descs, outs, impls, nbytes, flops = [], [], {}, 0, 0
+    tensors = []
+    for i, (name, N, K) in enumerate(LLAMA8B_LAYER):
+        x = session.randn((M, K), seed=1, dtype="bf16")
+        w = session.randn((N, K), seed=3 + i, std=0.02, dtype="bf16")
+        packed, scales, biases = A.quantize(w, bits=4, group_size=64, param_dtype="bf16")
+        del w
+        out = session.empty("f32", (M, N))
+        descs.append(ops._descriptor(x, packed, scales, biases, 4, 64, out, "auto", "backend_equivalent"))
+        impls[name] = A.selected_implementation(x, packed, scales, biases, bits=4, group_size=64)
+        tensors.append((x, packed, scales, biases, out))
+        nbytes += algorithmic_bytes(M, N, K, 4, 64, 2, 2)
+        flops += 2 * M * N * K
+
+    def launch_all():
+        for d in descs:
+            status = lib.affon_rocm_quantized_matmul(session._handle, ctypes.byref(d))
+            if status != 0:
+                from affon_amd import _native
+                raise RuntimeError(_native.last_error())
+
+    stream = ctypes.c_void_p(session.stream)
+    for _ in range(warmup):
+        launch_all()
+    session.synchronize()
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+    for _ in range(steps):
+        launch_all()
+    hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+    hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+    hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+    session.synchronize()
+    start, stop = hip.event(), hip.event()
+    hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+    hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+    hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+    hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+    ms = ctypes.c_float()
+    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+    hip.lib.hipGraphExecDestroy(exe)
+    hip.lib.hipGraphDestroy(graph)
+    t = ms.value / steps
+    tensors.clear()
+    return {"implementations": impls, "us_per_layer": round(t * 1e3, 2),
+            "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "TFLOP/s": round(flops / (t * 1e-3) / 1e12, 3), "algorithmic_bytes": nbytes}
+
+
 def copy_calibration(session) -> int:
     """Copies of a known size, profiled with the same byte counters as the
     kernels, give the factor from counter units to bytes."""
@@ -286,6 +347,12 @@ def main() -> int:
         if want(name):
             record(name, Workload(session, name, 512, N, K, 4, 64, policy="approximate"), bound="mfma")
             extras[name]["numerical_policy"] = "approximate"
+    if want("decode_4bit_g64_m16"):
+        record("decode_4bit_g64_m16", Workload(session, "decode_4bit_g64_m16", 16, 14336, 4096, 4, 64))
+    for M in (1, 32):
+        name = f"llama8b_layer_4bit_g64_m{M}"
+        if want(name):
+            extras[name] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup)
     if want("decode_4bit_g64_f32_4096"):
         record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
                                                     x_dtype="f32", p_dtype="f32"))

@@ -397,7 +397,7 @@ def test_gemv_mfma_exact_integer_products(session, bits, p_dtype, rng):
     output must equal the f64 reference exactly (partial column tiles, one or
     many K steps, split K)."""
     for M, N, K, group in [(1, 40, 256, 64), (2, 300, 1024, 128), (5, 129, 4096, 64), (16, 1000, 2048, 256),
-                           (16, 4096, 14336, 64)]:
+                           (16, 4096, 14336, 64), (17, 200, 1024, 64), (32, 1100, 4096, 128)]:
         q = rng.integers(0, 1 << bits, size=(N, K))
         x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
         s = 2.0 ** rng.integers(-3, 1, size=(N, K // group))
@@ -409,6 +409,16 @@ def test_gemv_mfma_exact_integer_products(session, bits, p_dtype, rng):
         out = session.empty("f32", (M, N))
         A.quantized_matmul_into(out, xt, wt, st, bt, bits=bits, group_size=group, implementation="gemv_mfma")
         np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
+
+
+@pytest.mark.parametrize("M", [24, 32])
+def test_gemv_mfma_two_row_blocks_against_oracle(session, M):
+    """M = 17..32 runs two blocks of 16 MFMA rows on shared decoded codes."""
+    x, packed, s, b = seeded_problem(M, 1024, 4096, 4, 64, "bf16", "bf16", seed=5)
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=64) == "rocm_quantized_matmul.gemv_mfma"
+    y = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=64)
+    check_against_oracle(y.numpy(), x, packed, s, b, 4, 64, True)
 
 
 def test_gemv_mfma_selected_for_decode_batches(session):
