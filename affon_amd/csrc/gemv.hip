@@ -260,7 +260,8 @@ bool gemv_supports(const QmmProblem& p) {
 
 bool gemv1_supports(const QmmProblem& p) {
   // One activation row, dense rows, 16-byte aligned packed rows and
-  // activations, every 16-byte chunk inside one group, LDS for the row.
+  // activations, every 16-byte chunk inside one group, LDS for the row (the
+  // one-row variant), parameters aligned to their element size.
   const int64_t cv = 128 / p.bits;
   const int xbytes = p.x_dtype == AFFON_ROCM_BF16 ? 2 : 4;
   if (p.M != 1 || p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
@@ -270,8 +271,11 @@ bool gemv1_supports(const QmmProblem& p) {
   if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0 || p.ws0 % 4 != 0) return false;
   if (reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return false;
   const int64_t chunks = p.K / cv;
-  const int64_t lds = (chunks * (cv * xbytes / 4 + 1) + 4) * 4;
-  return lds <= gemv1::kMaxLdsBytes && chunks <= gemv1::kMaxChunks;
+  const int pbytes = p.p_dtype == AFFON_ROCM_BF16 ? 2 : 4;
+  if (reinterpret_cast<uintptr_t>(p.s) % pbytes != 0 || reinterpret_cast<uintptr_t>(p.b) % pbytes != 0) return false;
+  if (chunks > gemv1::kMaxChunks) return false;
+  const size_t lds = gemv1::lds_size_for(static_cast<int>(cv * xbytes / 16), static_cast<int>(chunks), 1);
+  return lds <= static_cast<size_t>(gemv1::kMaxLdsBytes);
 }
 
 hipError_t gemv_launch(const QmmProblem& p, const Launch& l) {

@@ -9,8 +9,10 @@
 //     + 64*i, so one load instruction reads 1 KiB of contiguous packed words
 //     of one row; all R*CPL chunk loads (and the group parameters) are issued
 //     before anything waits;
-//   * the activation row is staged once per workgroup in LDS together with
-//     the sum of every chunk's activations; each wave copies its chunks into
+//   * the activation row is staged once per workgroup in LDS, 16 bytes per
+//     thread at a time, together with the sum of every chunk's activations;
+//     activation and parameter loads are issued before the packed words, so
+//     staging waits only for them; each wave copies its chunks into
 //     registers once and reuses them for its R rows;
 //   * codes are converted exactly (FP8 conversions for 2/4-bit codes,
 //     v_cvt_f32_ubyte for 8-bit codes) and multiplied with v_dot2_f32_bf16
@@ -50,6 +52,32 @@ struct Args {
 
 template <int BITS>
 constexpr int chunk_values() { return 128 / BITS; }
+
+// Activations of one chunk as staged in LDS: kPieces 16-byte pieces (2..16).
+// Piece j of chunk c sits in slot j at uint4 index j * stride + (c ^ swizzle
+// (j)), stride = chunks rounded up to 16. The swizzle spreads the pieces that
+// one 16-lane LDS phase writes (kPieces consecutive pieces of 16 / kPieces
+// chunks) over all 64 banks, and keeps the compute phase's reads (one slot of
+// 16 consecutive chunks) conflict-free.
+template <int BITS, typename XT>
+struct XStage {
+  static constexpr int kDwords = chunk_values<BITS>() * XT::bytes / 4;  // per chunk
+  static constexpr int kPieces = kDwords / 4;
+  static constexpr int kPieceShift = kPieces == 2 ? 1 : kPieces == 4 ? 2 : kPieces == 8 ? 3 : 4;
+  static_assert((1 << kPieceShift) == kPieces, "pieces per chunk");
+  __host__ __device__ static constexpr int stride(int chunks) { return (chunks + 15) & ~15; }
+  __device__ static int slot(int c, int j, int stride) { return j * stride + (c ^ ((j * (16 / kPieces)) & 15)); }
+};
+
+// LDS of one workgroup: the staged activations, one f32 sum per chunk, then
+// kWaves * R K-part partials.
+__host__ __device__ constexpr size_t lds_size_for(int pieces_per_chunk, int chunks, int R) {
+  return static_cast<size_t>(pieces_per_chunk) * ((chunks + 15) & ~15) * 16 + (static_cast<size_t>(chunks) + kWaves * R) * 4;
+}
+template <int BITS, typename XT, int R>
+__host__ __device__ constexpr size_t lds_size(int chunks) {
+  return lds_size_for(XStage<BITS, XT>::kPieces, chunks, R);
+}
 
 __device__ __forceinline__ bf16x2_t pack2(float a, float b) { return bf16x2_t{static_cast<__bf16>(a), static_cast<__bf16>(b)}; }
 
@@ -101,6 +129,16 @@ __device__ __forceinline__ int code_k(int t, int j) {
   return BITS == 4 ? 2 * j + t : 4 * j + t;
 }
 
+// Staged bf16 dword (within a chunk) that holds the activations of the code
+// pair (bytes 2h, 2h+1 of mask t) of word i. Each 16-byte piece of staged
+// activations holds the pairs of 8 consecutive k, so staging is local to a
+// piece: 4-bit pieces are words (pairs (0,2) (4,6) (1,3) (5,7)), 2-bit pieces
+// are half words (pairs (0,4) (1,5) (2,6) (3,7)).
+template <int BITS>
+__device__ __forceinline__ int pair_slot(int i, int t, int h) {
+  return BITS == 4 ? i * 4 + 2 * t + h : i * 8 + 4 * h + t;
+}
+
 // Sum over one 16-byte chunk (4 words) of x*q in units of the code step
 // (fp8 path) or exactly (8-bit path). xr holds the chunk's activations as
 // staged: bf16 pairs, or f32 values in k order.
@@ -134,7 +172,7 @@ __device__ __forceinline__ float chunk_dot(const uint32_t* words, const uint32_t
         for (int h = 0; h < 2; ++h) {
           if constexpr (XT::bytes == 2) {
             acc = __builtin_amdgcn_fdot2_f32_bf16(fp8_pair_bf16(m, h == 1),
-                                                  __builtin_bit_cast(bf16x2_t, xr[i * (P / 2) + 2 * t + h]), acc,
+                                                  __builtin_bit_cast(bf16x2_t, xr[pair_slot<BITS>(i, t, h)]), acc,
                                                   false);
           } else {
             const f32x2_t q = fp8_pair_f32(m, h == 1);
@@ -148,27 +186,20 @@ __device__ __forceinline__ float chunk_dot(const uint32_t* words, const uint32_t
   return acc;
 }
 
-// Writes one chunk of bf16 activations (src: CV values in k order) into the
-// pair order chunk_dot consumes and returns the sum of the chunk.
+// Low (high) bf16 halves of dwords a and b as one pair: a's in the low half.
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+// One 16-byte piece of bf16 activations (8 consecutive k) in the pair order
+// chunk_dot consumes (pair_slot).
 template <int BITS>
-__device__ __forceinline__ void permute_bf16_chunk(const uint32_t* src, uint32_t* dst) {
-  constexpr int P = 32 / BITS;
-  auto value = [&](int k) -> uint32_t { return (src[k >> 1] >> (16 * (k & 1))) & 0xffffu; };
+__device__ __forceinline__ u32x4_t permute_bf16_piece(u32x4_t d) {
   if constexpr (BITS == 8) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = src[i];
+    return d;
+  } else if constexpr (BITS == 4) {
+    return u32x4_t{pair_lo(d.x, d.y), pair_lo(d.z, d.w), pair_hi(d.x, d.y), pair_hi(d.z, d.w)};
   } else {
-    constexpr int T = BITS == 4 ? 2 : 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int k0 = i * P + code_k<BITS>(t, 2 * h);
-          const int k1 = i * P + code_k<BITS>(t, 2 * h + 1);
-          dst[i * (P / 2) + 2 * t + h] = value(k0) | (value(k1) << 16);
-        }
+    return u32x4_t{pair_lo(d.x, d.z), pair_hi(d.x, d.z), pair_lo(d.y, d.w), pair_hi(d.y, d.w)};
   }
 }
 
@@ -192,16 +223,59 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// Sum of v over aligned groups of G consecutive lanes (G = 2..16), in every
+// lane of the group: quad swaps, then the half-row mirror (lane i of 8 reads
+// lane 7-i, so each quad adds the other) and the row mirror (i of 16 reads
+// 15-i).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp<0xb1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v += dpp<0x4e>(v);   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += dpp<0x141>(v);  // row_half_mirror
+  if constexpr (G >= 16) v += dpp<0x140>(v); // row_mirror
+  return v;
+}
+
+// Stages the 64 pieces base .. base+63 of the activation row (lane order;
+// pieces >= count are absent) into LDS: the permuted piece into its slot and
+// the chunk's sum into xsum. The whole wave calls it (the group sums read
+// neighbouring lanes).
+template <int BITS, typename XT>
+__device__ __forceinline__ void stage_pieces(u32x4_t v, int p, int count, uint4* xs, float* xsum, int stride) {
+  using XS = XStage<BITS, XT>;
+  const bool valid = p < count;
+  u32x4_t o;
+  float sum;
+  if constexpr (XT::bytes == 2) {
+    o = permute_bf16_piece<BITS>(v);
+    // (Elements are copied to scalars first: a bit cast applied directly to a
+    // vector element reads element 0 with this compiler.)
+    const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+    const uint32_t o0 = o.x, o1 = o.y, o2 = o.z, o3 = o.w;
+    sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o0), ones, 0.0f, false);
+    sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o1), ones, sum, false);
+    sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o2), ones, sum, false);
+    sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, o3), ones, sum, false);
+  } else {
+    o = v;
+    sum = (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
+  }
+  sum = group_sum<XS::kPieces>(valid ? sum : 0.0f);
+  const int c = p >> XS::kPieceShift, j = p & (XS::kPieces - 1);
+  if (valid) {
+    xs[XS::slot(c, j, stride)] = make_uint4(o.x, o.y, o.z, o.w);
+    if (j == 0) xsum[c] = sum;
+  }
+}
+
 template <int BITS, typename XT, typename PT, int R, int CPL>
 __global__ __launch_bounds__(kThreads) void kernel(Args a) {
-  constexpr int CV = chunk_values<BITS>();
-  constexpr int XDW = CV * XT::bytes / 4;  // dwords of activations per chunk
-  // LDS: the activation row, slot-major (16-byte slot j of chunk c at
-  // uint4 index j*chunks + c, so lanes reading consecutive chunks hit
-  // consecutive banks), then one f32 sum per chunk, then the K-part partials.
+  using XS = XStage<BITS, XT>;
+  constexpr int XDW = XS::kDwords;
   extern __shared__ uint32_t smem[];
+  const int stride = XS::stride(a.chunks);
   uint4* xs_lds = reinterpret_cast<uint4*>(smem);
-  float* xsum_lds = reinterpret_cast<float*>(smem + a.chunks * XDW);
+  float* xsum_lds = reinterpret_cast<float*>(smem + XS::kPieces * stride * 4);
   float* red = xsum_lds + a.chunks;
 
   // The wave index is uniform; reading it into a scalar register keeps all
@@ -212,17 +286,50 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * R;
   const int c_begin = kp * a.part;
   const int c_end = min(a.chunks, c_begin + a.part);
+  auto clamp_row = [&](int64_t n) { return n < a.N ? n : a.N - 1; };
 
-  // 1. Issue every packed-word and parameter load of this wave.
+  // 1. Loads, in the order their data is needed (the load counter drains in
+  //    order): the activation pieces this thread stages, the group parameters
+  //    of its chunks, then the packed words.
+  constexpr int kEarly = 8;  // pieces per thread loaded before the packed words
+  const int pieces = a.chunks * XS::kPieces;
+  const int wave_piece = wave * 64;
+  u32x4_t xp[kEarly];
+#pragma unroll
+  for (int e = 0; e < kEarly; ++e) {
+    const int p = wave_piece + e * kThreads + lane;
+    if (p < pieces) xp[e] = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(p) * 16u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Group parameters: one per (row, chunk); rows have uniform bases, lanes a
+  // 32-bit byte offset shared by all rows.
+  uint32_t sraw[R][CPL], braw[R][CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = c_begin + lane + 64 * i;
+    const uint32_t goff = static_cast<uint32_t>((c < c_end ? c : 0) >> a.cpg_shift) * PT::bytes;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = clamp_row(n0 + r);
+      const uint8_t* srow = a.s + n * a.ss0 * PT::bytes;
+      const uint8_t* brow = a.b + n * a.bs0 * PT::bytes;
+      if constexpr (PT::bytes == 2) {
+        sraw[r][i] = *reinterpret_cast<const uint16_t*>(srow + goff);
+        braw[r][i] = *reinterpret_cast<const uint16_t*>(brow + goff);
+      } else {
+        sraw[r][i] = *reinterpret_cast<const uint32_t*>(srow + goff);
+        braw[r][i] = *reinterpret_cast<const uint32_t*>(brow + goff);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   uint32_t wv[R][CPL][4];
-  float sv[R][CPL], bv[R][CPL];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    // Row bases are wave-uniform (scalar registers); lane offsets are 32-bit.
-    const int64_t n = n0 + r < a.N ? n0 + r : a.N - 1;
+    const int64_t n = clamp_row(n0 + r);
     const u32x4_t* row = reinterpret_cast<const u32x4_t*>(a.w + n * a.ws0);
-    const uint8_t* srow = a.s + n * a.ss0 * PT::bytes;
-    const uint8_t* brow = a.b + n * a.bs0 * PT::bytes;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = c_begin + lane + 64 * i;
@@ -232,44 +339,23 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
       wv[r][i][1] = v.y;
       wv[r][i][2] = v.z;
       wv[r][i][3] = v.w;
-      const int g = cc >> a.cpg_shift;
-      sv[r][i] = PT::load(srow, g);
-      bv[r][i] = PT::load(brow, g);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // 2. Stage the activation row (bf16: in chunk_dot pair order) and the sum
-  //    of every chunk in LDS.
-  for (int c = threadIdx.x; c < a.chunks; c += kThreads) {
-    const uint4* src = reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(c) * CV * XT::bytes);
-    uint32_t raw[XDW];
+  // 2. Stage the activation row and the chunk sums (waits only for the
+  //    activation loads). Rows longer than kEarly pieces per thread load the
+  //    rest here.
 #pragma unroll
-    for (int i = 0; i < XDW / 4; ++i) {
-      const uint4 v = src[i];
-      raw[4 * i] = v.x;
-      raw[4 * i + 1] = v.y;
-      raw[4 * i + 2] = v.z;
-      raw[4 * i + 3] = v.w;
-    }
-    uint32_t staged[XDW];
-    float sum = 0.0f;
-    if constexpr (XT::bytes == 2) {
-      permute_bf16_chunk<BITS>(raw, staged);
-      const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
-#pragma unroll
-      for (int i = 0; i < XDW; ++i)
-        sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, staged[i]), ones, sum, false);
-    } else {
-#pragma unroll
-      for (int i = 0; i < XDW; ++i) {
-        staged[i] = raw[i];
-        sum += __uint_as_float(raw[i]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < XDW / 4; ++i)
-      xs_lds[i * a.chunks + c] = make_uint4(staged[4 * i], staged[4 * i + 1], staged[4 * i + 2], staged[4 * i + 3]);
-    xsum_lds[c] = sum;
+  for (int e = 0; e < kEarly; ++e) {
+    const int base = wave_piece + e * kThreads;
+    if (base < pieces) stage_pieces<BITS, XT>(xp[e], base + lane, pieces, xs_lds, xsum_lds, stride);
+  }
+  for (int base = wave_piece + kEarly * kThreads; base < pieces; base += kThreads) {
+    const int p = base + lane;
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    if (p < pieces) v = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(p) * 16u);
+    stage_pieces<BITS, XT>(v, p, pieces, xs_lds, xsum_lds, stride);
   }
   __syncthreads();
 
@@ -277,6 +363,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   // Converted codes are n * unit; scales are divided by the unit (a power of
   // two, so exactly).
   const float inv_unit = BITS == 8 ? 1.0f : 1.0f / fp8_unit<XT>();
+  auto param = [](uint32_t raw) { return __uint_as_float(PT::bytes == 2 ? raw << 16 : raw); };
   float y[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) y[r] = 0.0f;
@@ -286,8 +373,8 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     if (c < c_end) {
       uint32_t xr[XDW];
 #pragma unroll
-      for (int j = 0; j < XDW / 4; ++j) {
-        const uint4 v = xs_lds[j * a.chunks + c];
+      for (int j = 0; j < XS::kPieces; ++j) {
+        const uint4 v = xs_lds[XS::slot(c, j, stride)];
         xr[4 * j] = v.x;
         xr[4 * j + 1] = v.y;
         xr[4 * j + 2] = v.z;
@@ -297,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const float acc = chunk_dot<BITS, XT>(wv[r][i], xr);
-        y[r] = fmaf(sv[r][i] * inv_unit, acc, fmaf(bv[r][i], xsum, y[r]));
+        y[r] = fmaf(param(sraw[r][i]) * inv_unit, acc, fmaf(param(braw[r][i]), xsum, y[r]));
       }
     }
   }
@@ -328,9 +415,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
 
 template <int BITS, typename XT, typename PT, int R, int CPL>
 hipError_t launch(const Args& a, hipStream_t stream) {
-  constexpr int CV = chunk_values<BITS>();
-  constexpr int XDW = CV * XT::bytes / 4;
-  const size_t lds = (static_cast<size_t>(a.chunks) * (XDW + 1) + kWaves * R) * 4;
+  const size_t lds = lds_size<BITS, XT, R>(a.chunks);
   const int64_t row_blocks = (a.N + R - 1) / R;
   const int64_t per_block = kWaves / a.ks;
   const unsigned blocks = static_cast<unsigned>((row_blocks + per_block - 1) / per_block);

@@ -33,8 +33,7 @@ struct Variant {
 
 template <int BITS, typename XT, int R>
 size_t lds_bytes(int chunks) {
-  constexpr int XDW = chunk_values<BITS>() * XT::bytes / 4;
-  return (static_cast<size_t>(chunks) * (XDW + 1) + kWaves * R) * 4;
+  return lds_size<BITS, XT, R>(chunks);
 }
 
 template <int BITS, typename XT, typename PT>
