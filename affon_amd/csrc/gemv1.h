@@ -115,6 +115,11 @@ __device__ __forceinline__ float fp8_unit() {
   }
 }
 
+// 1 / u for a power of two u, exactly: u = 0.5 * 2^e, so 1 / u = 2^(1 - e).
+__device__ __forceinline__ float pow2_reciprocal(float u) {
+  return __builtin_amdgcn_ldexpf(1.0f, 1 - __builtin_amdgcn_frexp_expf(u));
+}
+
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;
@@ -221,6 +226,54 @@ __device__ __forceinline__ float wave_sum(float v) {
   const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   return (r0 + r1) + (r2 + r3);
+}
+
+// Wave totals of R per-lane values (R = 1, 2, 4, 8), uniform. Rows are
+// paired first so that the lane reductions run on fewer registers:
+// permlane32_swap turns rows (2k, 2k+1) into one register holding row 2k's
+// 32-lane partials in lanes 0-31 and row 2k+1's in lanes 32-63;
+// permlane16_swap turns two such registers into one whose 16-lane groups hold
+// rows (4m, 4m+2, 4m+1, 4m+3). The 16-lane groups are then summed with DPP
+// and read out of lanes 0, 16, 32 and 48.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+template <int R>
+__device__ __forceinline__ void wave_totals(const float (&y)[R], float (&tot)[R]) {
+  if constexpr (R == 1) {
+    tot[0] = wave_sum(y[0]);
+  } else {
+    float h[R / 2];
+#pragma unroll
+    for (int k = 0; k < R / 2; ++k) {
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[2 * k]), __float_as_uint(y[2 * k + 1]), false,
+                                                      false);
+      h[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    if constexpr (R == 2) {
+      const float v = row_sum16(h[0]);
+      tot[0] = lane_value(v, 0) + lane_value(v, 16);
+      tot[1] = lane_value(v, 32) + lane_value(v, 48);
+    } else {
+#pragma unroll
+      for (int m = 0; m < R / 4; ++m) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(h[2 * m]), __float_as_uint(h[2 * m + 1]), false,
+                                                        false);
+        const float v = row_sum16(__uint_as_float(p[0]) + __uint_as_float(p[1]));
+        tot[4 * m] = lane_value(v, 0);
+        tot[4 * m + 2] = lane_value(v, 16);
+        tot[4 * m + 1] = lane_value(v, 32);
+        tot[4 * m + 3] = lane_value(v, 48);
+      }
+    }
+  }
 }
 
 // Sum of v over aligned groups of G consecutive lanes (G = 2..16), in every
@@ -362,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   // 3. Decode, multiply, apply group parameters per chunk.
   // Converted codes are n * unit; scales are divided by the unit (a power of
   // two, so exactly).
-  const float inv_unit = BITS == 8 ? 1.0f : 1.0f / fp8_unit<XT>();
+  const float inv_unit = BITS == 8 ? 1.0f : pow2_reciprocal(fp8_unit<XT>());
   auto param = [](uint32_t raw) { return __uint_as_float(PT::bytes == 2 ? raw << 16 : raw); };
   float y[R];
 #pragma unroll
@@ -390,8 +443,12 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
 
   // 4. Reduce across the wave, then across K-parts.
+  {
+    float tot[R];
+    wave_totals<R>(y, tot);
 #pragma unroll
-  for (int r = 0; r < R; ++r) y[r] = wave_sum(y[r]);
+    for (int r = 0; r < R; ++r) y[r] = tot[r];
+  }
   if (a.ks == 1) {
     if (lane < R) {
       float v = y[0];

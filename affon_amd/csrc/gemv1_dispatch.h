@@ -5,9 +5,9 @@
 // one that runs in the fewest rounds of resident waves (occupancy from the
 // compiled kernel), then with the fewest K-parts (no LDS reduction and
 // barrier), then with the most waves (more latency hiding). On MI355X this
-// picks the fastest or a variant within 6% of it on every decode shape of
-// the benchmark sweep (8/4-bit 14336x4096, 4096x14336, 4096x4096 f32,
-// 1024x4096, 128256x4096).
+// picks the fastest variant, or one within 3% of it, on each of 8-bit
+// 14336x4096 and 4096x14336, 4-bit 14336x4096, 4096x14336, 4096x4096,
+// 1024x4096 and 128256x4096 (bf16), and 4-bit 4096x4096 with f32 operands.
 #pragma once
 
 #include <map>
@@ -43,8 +43,8 @@ const Variant* variants(int* count) {
    lds_bytes<BITS, XT, R>}
   static const Variant table[] = {
       AFFON_GEMV1_VARIANT(1, 1), AFFON_GEMV1_VARIANT(2, 1), AFFON_GEMV1_VARIANT(4, 1), AFFON_GEMV1_VARIANT(8, 1),
-      AFFON_GEMV1_VARIANT(1, 2), AFFON_GEMV1_VARIANT(2, 2), AFFON_GEMV1_VARIANT(4, 2), AFFON_GEMV1_VARIANT(2, 4),
-      AFFON_GEMV1_VARIANT(4, 4),
+      AFFON_GEMV1_VARIANT(1, 2), AFFON_GEMV1_VARIANT(2, 2), AFFON_GEMV1_VARIANT(4, 2), AFFON_GEMV1_VARIANT(1, 4),
+      AFFON_GEMV1_VARIANT(2, 4), AFFON_GEMV1_VARIANT(4, 4),
   };
 #undef AFFON_GEMV1_VARIANT
   *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
