@@ -411,6 +411,48 @@ def test_gemv_mfma_exact_integer_products(session, bits, p_dtype, rng):
         np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
 
 
+VROW_CASES = {  # (M, N, K, group): one to four activation rows, each group-per-set layout, one to four K-parts
+    8: [(1, 77, 1024, 64), (2, 300, 512, 32), (3, 129, 1024, 16), (4, 1000, 2048, 64), (4, 64, 4096, 32)],
+    4: [(1, 77, 4096, 64), (2, 300, 1024, 128), (3, 129, 512, 32), (4, 1000, 2048, 64), (1, 40, 8192, 128)],
+    2: [(1, 77, 1024, 64), (2, 300, 2048, 128), (4, 129, 4096, 64), (3, 50, 1024, 128)],
+}
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("p_dtype", ["bf16", "f32"])
+def test_virtual_row_decode_exact_integer_products(session, bits, p_dtype, rng):
+    """M <= 4 decode on the matrix cores with groups separated by masked
+    A-operand rows: integer codes and activations with power-of-two scales and
+    integer biases make every partial sum exact, so the output must equal the
+    f64 reference exactly. Partial 16-row blocks (N % 16 != 0), 1-4 groups per
+    set of four 16-byte chunks, and 1, 2 or 4 K-parts per row."""
+    for M, N, K, group in VROW_CASES[bits]:
+        q = rng.integers(0, 1 << bits, size=(N, K))
+        x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
+        s = 2.0 ** rng.integers(-3, 1, size=(N, K // group))
+        b = rng.integers(-2, 3, size=(N, K // group)).astype(np.float64)
+        expected = reference_f64(x, q, s, b, group)
+        xt = upload(session, storage(x, "bf16"), "bf16")
+        wt = upload(session, pack_codes(q, bits), "u32")
+        st, bt = upload(session, storage(s, p_dtype), p_dtype), upload(session, storage(b, p_dtype), p_dtype)
+        out = session.empty("f32", (M, N))
+        A.quantized_matmul_into(out, xt, wt, st, bt, bits=bits, group_size=group, implementation="gemv_mfma")
+        np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
+
+
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_virtual_row_decode_against_oracle(session, M):
+    """Seeded N(0,1) activations and quantized N(0,0.02) weights, 4-bit and
+    8-bit group 64 at the decode sweep's row length: within the bf16
+    tolerance of the oracle."""
+    for bits in (4, 8):
+        x, packed, s, b = seeded_problem(M, 1100, 4096, bits, 64, "bf16", "bf16", seed=13)
+        xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+        assert A.selected_implementation(xt, wt, st, bt, bits=bits, group_size=64) == "rocm_quantized_matmul.gemv_mfma"
+        y = A.quantized_matmul(xt, wt, st, bt, bits=bits, group_size=64)
+        check_against_oracle(y.numpy(), x, packed, s, b, bits, 64, True)
+
+
 @pytest.mark.parametrize("M", [24, 32])
 def test_gemv_mfma_two_row_blocks_against_oracle(session, M):
     """M = 17..32 runs two blocks of 16 MFMA rows on shared decoded codes."""
