@@ -17,6 +17,7 @@
 // the prefill GEMM (lds_pipeline.h).
 
 #include "lds_pipeline.h"
+#include "vrow16_dispatch.h"
 #include "vrow_dispatch.h"
 
 namespace affon {
@@ -285,13 +286,18 @@ hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
 
 }  // namespace
 
-bool vrow_supports(const QmmProblem& p) {
-  vrow::Plan pl;
-  return vrow::plan(p, &pl);
+// Which virtual-row layout runs a problem: 1 = 8 rows per wave, 2 = 16 rows
+// per wave, 0 = neither (the LDS-tiled kernel below).
+int vrow_layout(const QmmProblem& p) {
+  vrow::Plan eight;
+  vrow16::Plan sixteen;
+  if (vrow::plan(p, &eight)) return 1;
+  if (vrow16::plan(p, &sixteen)) return 2;
+  return 0;
 }
 
 bool gemv_mfma_supports(const QmmProblem& p) {
-  if (vrow_supports(p)) return true;
+  if (vrow_layout(p) != 0) return true;
   if (p.x_dtype != AFFON_ROCM_BF16 || p.M > kMaxRows) return false;
   if (p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
   // Each K step inside one group, groups addressed by shift.
@@ -308,14 +314,19 @@ bool gemv_mfma_supports(const QmmProblem& p) {
 }
 
 hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
-  // M <= 4: the virtual-row kernel (packed words straight into the B
-  // operand, no LDS for weights); larger batches: the LDS-tiled kernel.
-  if (vrow_supports(p)) {
-    switch (p.bits) {
-      case 2: return vrow_launch_b2(p, l.stream);
-      case 4: return vrow_launch_b4(p, l.stream);
-      default: return vrow_launch_b8(p, l.stream);
-    }
+  // M <= 4: a virtual-row kernel (packed words straight into the B operand,
+  // no LDS for weights); larger batches: the LDS-tiled kernel.
+  switch (vrow_layout(p)) {
+    case 1:
+      return vrow_launch_b8(p, l.stream);
+    case 2:
+      switch (p.bits) {
+        case 2: return vrow16_launch_b2(p, l.stream);
+        case 4: return vrow16_launch_b4(p, l.stream);
+        default: return vrow16_launch_b8(p, l.stream);
+      }
+    default:
+      break;
   }
   TileArgs a;
   a.x = reinterpret_cast<const uint16_t*>(p.x);

@@ -411,21 +411,24 @@ def test_gemv_mfma_exact_integer_products(session, bits, p_dtype, rng):
         np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
 
 
-VROW_CASES = {  # (M, N, K, group): one to four activation rows, each group-per-set layout, one to four K-parts
-    8: [(1, 77, 1024, 64), (2, 300, 512, 32), (3, 129, 1024, 16), (4, 1000, 2048, 64), (4, 64, 4096, 32)],
-    4: [(1, 77, 4096, 64), (2, 300, 1024, 128), (3, 129, 512, 32), (4, 1000, 2048, 64), (1, 40, 8192, 128)],
-    2: [(1, 77, 1024, 64), (2, 300, 2048, 128), (4, 129, 4096, 64), (3, 50, 1024, 128)],
+VROW_CASES = {  # (M, N, K, group)
+    8: [(1, 77, 1024, 64), (2, 300, 512, 32), (2, 129, 2048, 16), (4, 1000, 2048, 64), (8, 64, 4096, 64),
+        (6, 200, 1024, 64)],
+    4: [(1, 77, 4096, 64), (2, 300, 1024, 128), (1, 129, 1024, 32), (4, 1000, 2048, 64), (8, 40, 8192, 128),
+        (5, 50, 4096, 128)],
+    2: [(1, 77, 2048, 64), (2, 300, 2048, 128), (4, 129, 4096, 128), (3, 50, 2048, 128)],
 }
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("p_dtype", ["bf16", "f32"])
 def test_virtual_row_decode_exact_integer_products(session, bits, p_dtype, rng):
-    """M <= 4 decode on the matrix cores with groups separated by masked
-    A-operand rows: integer codes and activations with power-of-two scales and
+    """Small-M decode on the matrix cores (M <= 2 at 8 bits: the 8-row
+    virtual-row layout; M <= 4: the 16-row layout; larger M: the LDS-tiled
+    kernel): integer codes and activations with power-of-two scales and
     integer biases make every partial sum exact, so the output must equal the
-    f64 reference exactly. Partial 16-row blocks (N % 16 != 0), 1-4 groups per
-    set of four 16-byte chunks, and 1, 2 or 4 K-parts per row."""
+    f64 reference exactly. Partial row blocks, 1-4 groups per MFMA span, and
+    1, 2 or 4 K-parts per row."""
     for M, N, K, group in VROW_CASES[bits]:
         q = rng.integers(0, 1 << bits, size=(N, K))
         x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
@@ -440,7 +443,7 @@ def test_virtual_row_decode_exact_integer_products(session, bits, p_dtype, rng):
         np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
 
 
-@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("M", [2, 3, 4, 8])
 def test_virtual_row_decode_against_oracle(session, M):
     """Seeded N(0,1) activations and quantized N(0,0.02) weights, 4-bit and
     8-bit group 64 at the decode sweep's row length: within the bf16
