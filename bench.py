@@ -347,6 +347,12 @@ def main() -> int:
         if want(name):
             record(name, Workload(session, name, 512, N, K, 4, 64, policy="approximate"), bound="mfma")
             extras[name]["numerical_policy"] = "approximate"
+    # Large prefill stress: 4-bit group 32, 2048 activation rows, both weight orientations.
+    for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192", 28672, 8192),
+                       ("prefill_4bit_g32_m2048_n8192_k28672", 8192, 28672)):
+        if want(name):
+            record(name, Workload(session, name, 2048, N, K, 4, 32, policy="approximate"), bound="mfma")
+            extras[name]["numerical_policy"] = "approximate"
     if want("decode_4bit_g64_m16"):
         record("decode_4bit_g64_m16", Workload(session, "decode_4bit_g64_m16", 16, 14336, 4096, 4, 64))
     for M in (1, 32):

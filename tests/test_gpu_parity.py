@@ -550,6 +550,29 @@ def test_quantize_full_size_stress_bit_exact(session):
     np.testing.assert_array_equal(biases.storage(), expected[2])
 
 
+def test_prefill_stress_full_size_sampled(session):
+    """Large prefill stress: x bf16 [2048, 8192], 4-bit group 32, bf16
+    parameters, W [28672, 8192] and W [8192, 28672] (the same seeded values in
+    both shapes), quantized on the GPU (bit-exactness of that quantize: the
+    test above). The full outputs are checked on sampled activation rows and
+    column ranges against the oracle, within the bf16-input tolerance."""
+    wf, _ = O.randn(2, 28672 * 8192, 0.0, 0.02)
+    _, xb = O.randn(1, 2048 * 8192, 0.0, 1.0)
+    x = xb.reshape(2048, 8192)
+    xt = upload(session, x, "bf16")
+    rows = [0, 777, 2047]
+    for N, K in ((28672, 8192), (8192, 28672)):
+        w = wf.reshape(N, K)
+        packed, scales, biases = A.quantize(upload(session, w, "f32"), bits=4, group_size=32, param_dtype="bf16")
+        if K != 8192:  # activations of the second orientation: the seeded rows repeated to K columns
+            xt = upload(session, np.ascontiguousarray(np.tile(x, (1, -(-K // 8192)))[:, :K]), "bf16")
+        y = run_mfma(session, xt, packed, scales, biases, 4, 32)
+        xs = xt.storage()[rows]
+        pk, sc, bi = packed.storage(), scales.storage(), biases.storage()
+        for n_range in ((0, 256), (N - 256, N)):
+            check_against_oracle(y[rows], xs, pk, sc, bi, 4, 32, True, n_range=n_range)
+
+
 # ---- boundary behaviour -------------------------------------------------------------------
 
 def test_drop_in_host_pointer_entry_point():
