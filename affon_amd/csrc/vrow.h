@@ -30,6 +30,8 @@
 // decode kernels.
 #pragma once
 
+#include <atomic>
+
 #include "gemv1.h"
 #include "lds_pipeline.h"
 
@@ -356,12 +358,19 @@ hipError_t launch(const Args& a, hipStream_t stream) {
   const int64_t per_block = kWaves / a.ks;
   const unsigned blocks = static_cast<unsigned>((row_blocks + per_block - 1) / per_block);
   if (lds > 64 * 1024) {
-    // Dynamic LDS beyond 64 KB must be allowed per kernel (once; not a
-    // stream operation, so it is also safe under graph capture).
-    static const hipError_t allowed = hipFuncSetAttribute(reinterpret_cast<const void*>(&kernel<BITS, PT, MP, GH, CPL>),
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                          static_cast<int>(kMaxLdsBytes));
-    if (allowed != hipSuccess) return allowed;
+    // Dynamic LDS beyond 64 KB must be allowed per kernel and device (once
+    // each; not a stream operation, so it is also safe under graph capture).
+    static std::atomic<uint64_t> allowed_devices{0};
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = device < 64 ? uint64_t(1) << device : 0;
+    if (bit == 0 || (allowed_devices.load() & bit) == 0) {
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&kernel<BITS, PT, MP, GH, CPL>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxLdsBytes));
+      if (e != hipSuccess) return e;
+      allowed_devices.fetch_or(bit);
+    }
   }
   hipLaunchKernelGGL((kernel<BITS, PT, MP, GH, CPL>), dim3(blocks), dim3(kThreads), lds, stream, a);
   return hipGetLastError();

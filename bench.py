@@ -193,6 +193,64 @@ def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0) -> 
             "max_abs_err_vs_gpu": err}
 
 
+def cpu_baseline_parallel(work: Workload, gpu_out: np.ndarray, seconds: float = 5.0) -> dict:
+    """The same oracle loop split over output columns on the host's cores
+    (threads; the C call releases the interpreter lock), repeated whole
+    passes for about `seconds`: the multi-core CPU figure beside the
+    single-threaded one. Checks its output against the GPU's."""
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import oracle as O
+    x, packed, scales, biases = work.host_operands()
+    M, N = work.M, work.N
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(16, cores, N))
+    bounds = [(N * i // threads, N * (i + 1) // threads) for i in range(threads)]
+    out = np.zeros((M, N), dtype=np.float32)
+
+    def one_pass(pool):
+        list(pool.map(lambda r: O.quantized_matmul(x, packed, scales, biases, work.bits, work.group,
+                                                   n_range=r, out=out), bounds))
+
+    with ThreadPoolExecutor(threads) as pool:
+        t0 = time.perf_counter()
+        one_pass(pool)
+        first = time.perf_counter() - t0
+        passes = max(1, int(seconds / max(first, 1e-9)))
+        t0 = time.perf_counter()
+        for _ in range(passes):
+            one_pass(pool)
+        elapsed = time.perf_counter() - t0
+    err = float(np.abs(gpu_out.astype(np.float64) - out).max())
+    return {"value": round(passes * work.bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle scalar quantized_matmul split over output columns, {passes} whole passes, "
+                      f"{elapsed:.1f} s on {threads} threads",
+            "max_abs_err_vs_gpu": err}
+
+
+def end_to_end(work: Workload, calls: int = 200) -> dict:
+    """One call as the reference's benchmark times it: launch, then read the
+    output back to the host (the host read synchronises), per call, from
+    this Python caller."""
+    out_ptr = ctypes.c_void_p(work.out.data_ptr)
+    host = np.empty(work.M * work.N, dtype=np.float32)
+    nbytes = host.nbytes
+
+    def call(i):
+        work.launch(i)
+        status = work.lib.affon_rocm_memcpy_d2h(work.session._handle, host.ctypes.data, out_ptr, nbytes)
+        if status != 0:
+            raise RuntimeError("readback failed")
+
+    for i in range(10):
+        call(i)
+    t0 = time.perf_counter()
+    for i in range(calls):
+        call(i)
+    us = (time.perf_counter() - t0) / calls * 1e6
+    return {"us_per_call": round(us, 2), "GB/s": round(work.bytes / (us * 1e-6) / 1e9, 1), "calls": calls,
+            "includes": "launch + device-to-host copy of the output, synchronous, Python caller"}
+
+
 def roofline_gemv(work: Workload, ms: float, traffic) -> dict:
     achieved = work.bytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -317,9 +375,11 @@ def main() -> int:
     impl = main_work.implementation
     sets = main_work.sets
     baseline = cpu_baseline(main_work, gpu_out, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    extras = {"decode_8bit_g64_m1_end_to_end": end_to_end(main_work)}
+    if args.cpu_seconds > 0:
+        extras["cpu_baseline_parallel"] = cpu_baseline_parallel(main_work, gpu_out, args.cpu_seconds / 2)
     main_work.release()
 
-    extras = {}
     only = set(filter(None, args.only.split(",")))
 
     def want(name):
