@@ -573,6 +573,42 @@ def test_prefill_stress_full_size_sampled(session):
             check_against_oracle(y[rows], xs, pk, sc, bi, 4, 32, True, n_range=n_range)
 
 
+def test_checkpoint_adapter_quantized_linears(session, tmp_path, rng):
+    """MLX-affine checkpoint layers loaded onto the device: one shaped like the
+    reference's checkpoint evidence (8-bit group 64, U32 [2048,256] with BF16
+    [2048,16] scales/biases, docs/core/quantized-inference.md:89-96), one
+    4-bit group 64 layer, one U32 tensor without parameters (not a layer).
+    Loaded storage is bit-identical to the file, and each layer applied to the
+    reference tool's activations ((c*7 + r*3) % 31 - 15)/16
+    (tools/test-quantized-checkpoint.py:53) matches the oracle."""
+    from affon_amd import checkpoint as C
+    from tests.test_checkpoint import write_file
+    layers = {"talker.lm_head.0": (8, 2048, 1024), "talker.proj": (4, 300, 512)}
+    entries, arrays = [], {}
+    for prefix, (bits, out, inp) in layers.items():
+        q = rng.integers(0, 1 << bits, size=(out, inp))
+        s = O.bf16_from_f32(rng.uniform(0.001, 0.01, size=(out, inp // 64)).astype(np.float32))
+        b = O.bf16_from_f32(rng.uniform(-0.5, 0.5, size=(out, inp // 64)).astype(np.float32))
+        arrays[prefix] = (pack_codes(q, bits), s, b)
+        entries += [(prefix + ".weight", "U32", [out, inp * bits // 32], arrays[prefix][0].tobytes()),
+                    (prefix + ".scales", "BF16", list(s.shape), s.tobytes()),
+                    (prefix + ".biases", "BF16", list(b.shape), b.tobytes())]
+    entries.append(("talker.codebook.weight", "U32", [16, 4], np.arange(64, dtype=np.uint32).tobytes()))
+    path = str(write_file(tmp_path / "model.safetensors", entries, metadata={"format": "mlx"}))
+    for prefix, (bits, out, inp) in layers.items():
+        bound = C.quantized_linears(session, path, bits=bits, group_size=64, prefixes=[prefix])[prefix]
+        assert (bound.out_features, bound.in_features) == (out, inp)
+        for tensor, expected in zip((bound.packed, bound.scales, bound.biases), arrays[prefix]):
+            np.testing.assert_array_equal(tensor.storage(), expected)
+        x = np.array([[((c * 7 + r * 3) % 31 - 15) / 16 for c in range(inp)] for r in range(3)], np.float32)
+        y = bound(session.tensor(x, "f32")).numpy()
+        check_against_oracle(y, x, *arrays[prefix], bits, 64, False)
+    with pytest.raises(C.CheckpointError, match="shapes do not match"):
+        C.quantized_linears(session, path, bits=4, group_size=64)  # the 8-bit layer read as 4-bit
+    t = C.load(session, path, ["talker.codebook.weight"])["talker.codebook.weight"]
+    np.testing.assert_array_equal(t.storage(), np.arange(64, dtype=np.uint32).reshape(16, 4))
+
+
 # ---- boundary behaviour -------------------------------------------------------------------
 
 def test_drop_in_host_pointer_entry_point():
