@@ -47,6 +47,21 @@ class QmmDesc(ctypes.Structure):
     ]
 
 
+EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_SILU_GATE = 0, 1, 2
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [
+        ("kind", c_int32),
+        ("bias", c_void_p),
+        ("bias_bytes", c_size_t),
+        ("bias_dtype", c_int32),
+        ("up_packed", View),
+        ("up_scales", View),
+        ("up_biases", View),
+    ]
+
+
 SIGNATURES = {
     "affon_rocm_device_count": (c_int, [ctypes.POINTER(c_int)]),
     "affon_rocm_session_create": (c_int, [c_int, ctypes.POINTER(c_void_p)]),
@@ -61,6 +76,9 @@ SIGNATURES = {
     "affon_rocm_last_error": (c_char_p, []),
     "affon_rocm_quantized_matmul": (c_int, [c_void_p, ctypes.POINTER(QmmDesc)]),
     "affon_rocm_quantized_matmul_select": (c_int, [ctypes.POINTER(QmmDesc), c_char_p, c_size_t]),
+    "affon_rocm_quantized_matmul_fused": (c_int, [c_void_p, ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue)]),
+    "affon_rocm_quantized_matmul_fused_select": (c_int, [ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue), c_char_p,
+                                                         c_size_t]),
     "affon_rocm_quantized_matmul_capabilities": (c_char_p, []),
     "compute_core_run_quantized_matmul_f32": (c_int, [
         c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t,

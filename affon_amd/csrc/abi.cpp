@@ -397,6 +397,132 @@ int affon_rocm_quantized_matmul_select(const affon_rocm_qmm_desc* desc, char* id
   return AFFON_ROCM_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// How a fused call runs: the first problem (the only one, or the gate
+// projection), and for a two-launch SiLU gate the up projection, whose
+// kernel multiplies silu(stored gate) into its output.
+struct FusedPlan {
+  affon::QmmProblem first, second;
+  const Candidate* first_c = nullptr;
+  const Candidate* second_c = nullptr;
+  bool two = false;
+};
+
+bool same_layout(const affon_rocm_view& a, const affon_rocm_view& b) {
+  return a.stride[0] == b.stride[0] && a.stride[1] == b.stride[1];
+}
+
+int plan_fused(const affon_rocm_qmm_desc* d, const affon_rocm_qmm_epilogue* e, FusedPlan* plan) {
+  if (e == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul epilogue is null");
+  int status = validate(d, &plan->first);
+  if (status != AFFON_ROCM_OK) return status;
+  affon::QmmProblem& p = plan->first;
+  switch (e->kind) {
+    case AFFON_ROCM_EPILOGUE_NONE:
+      return select(d, p, &plan->first_c);
+    case AFFON_ROCM_EPILOGUE_BIAS: {
+      const int esize = element_size(e->bias_dtype);
+      if (e->bias == nullptr || !is_float_dtype(e->bias_dtype))
+        return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul output bias must be an f32/bf16 vector");
+      if (e->bias_bytes / static_cast<size_t>(esize) < static_cast<size_t>(p.N) ||
+          reinterpret_cast<uintptr_t>(e->bias) % static_cast<uintptr_t>(esize) != 0)
+        return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul output bias needs N aligned elements");
+      p.epi.kind = affon::kEpiBias;
+      p.epi.bias = static_cast<const uint8_t*>(e->bias);
+      p.epi.bias_bf16 = e->bias_dtype == AFFON_ROCM_BF16;
+      return select(d, p, &plan->first_c);
+    }
+    case AFFON_ROCM_EPILOGUE_SILU_GATE: {
+      const affon_rocm_view* gate[3] = {&d->packed, &d->scales, &d->biases};
+      const affon_rocm_view* up[3] = {&e->up_packed, &e->up_scales, &e->up_biases};
+      const char* names[3] = {"up packed", "up scales", "up biases"};
+      for (int i = 0; i < 3; ++i) {
+        if (up[i]->dtype != gate[i]->dtype || up[i]->shape[0] != gate[i]->shape[0] ||
+            up[i]->shape[1] != gate[i]->shape[1])
+          return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul %s must match the gate projection's shape and dtype",
+                      names[i]);
+        if ((status = check_view(*up[i], names[i])) != AFFON_ROCM_OK) return status;
+      }
+      affon::QmmProblem& q = plan->second;
+      q = p;
+      q.w = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(e->up_packed.data) +
+                                              e->up_packed.byte_offset);
+      q.ws0 = e->up_packed.stride[0];
+      q.ws1 = e->up_packed.stride[1];
+      q.s = static_cast<const uint8_t*>(e->up_scales.data) + e->up_scales.byte_offset;
+      q.ss0 = e->up_scales.stride[0];
+      q.ss1 = e->up_scales.stride[1];
+      q.b = static_cast<const uint8_t*>(e->up_biases.data) + e->up_biases.byte_offset;
+      q.bs0 = e->up_biases.stride[0];
+      q.bs1 = e->up_biases.stride[1];
+      if ((status = select(d, p, &plan->first_c)) != AFFON_ROCM_OK) return status;
+      // One launch when the gate's kernel pairs rows of both projections.
+      affon::QmmProblem paired = p;
+      paired.epi.kind = affon::kEpiSiluPair;
+      paired.epi.w2 = q.w;
+      paired.epi.s2 = q.s;
+      paired.epi.b2 = q.b;
+      if (plan->first_c->impl == AFFON_ROCM_IMPL_GEMV && same_layout(d->packed, e->up_packed) &&
+          same_layout(d->scales, e->up_scales) && same_layout(d->biases, e->up_biases) &&
+          affon::gemv_pair_supports(paired)) {
+        p = paired;
+        return AFFON_ROCM_OK;
+      }
+      plan->two = true;
+      q.epi.kind = affon::kEpiGateMul;
+      return select(d, q, &plan->second_c);
+    }
+    default:
+      return fail(AFFON_ROCM_INVALID_SHAPE, "quantized_matmul unknown epilogue %d", e->kind);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int affon_rocm_quantized_matmul_fused(affon_rocm_session* session, const affon_rocm_qmm_desc* desc,
+                                      const affon_rocm_qmm_epilogue* epilogue) {
+  clear_error();
+  FusedPlan plan;
+  int status = plan_fused(desc, epilogue, &plan);
+  if (status != AFFON_ROCM_OK) return status;
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  affon::Launch launch;
+  launch.stream = session->stream;
+  launch.workspace = session->workspace;
+  hipError_t e = plan.first_c->launch(plan.first, launch);
+  if (e != hipSuccess) return hip_fail(e, plan.first_c->id);
+  if (plan.two) {
+    e = plan.second_c->launch(plan.second, launch);
+    if (e != hipSuccess) return hip_fail(e, plan.second_c->id);
+  }
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_quantized_matmul_fused_select(const affon_rocm_qmm_desc* desc, const affon_rocm_qmm_epilogue* epilogue,
+                                             char* id, size_t cap) {
+  clear_error();
+  FusedPlan plan;
+  int status = plan_fused(desc, epilogue, &plan);
+  if (status != AFFON_ROCM_OK) return status;
+  std::string text = plan.first_c->id;
+  switch (plan.first.epi.kind) {
+    case affon::kEpiBias: text += "[bias]"; break;
+    case affon::kEpiSiluPair: text += "[silu_gate]"; break;
+    default: break;
+  }
+  if (plan.two) text += std::string(";") + plan.second_c->id + "[gate_mul]";
+  if (id != nullptr && cap > 0) {
+    std::strncpy(id, text.c_str(), cap - 1);
+    id[cap - 1] = '\0';
+  }
+  return AFFON_ROCM_OK;
+}
+
 const char* affon_rocm_quantized_matmul_capabilities(void) {
   static const char* kJson =
       "["

@@ -283,12 +283,16 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(TileArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int row = m0 + 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
-          if (row < a.M && col < a.N) f(static_cast<int64_t>(row) * a.N + col, acc[mt][nt][v]);
+          if (row < a.M && col < a.N) f(static_cast<int64_t>(row) * a.N + col, col, acc[mt][nt][v]);
         }
     }
   };
-  float* dst = a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N;
-  for_each_output([&](int64_t i, float v) { dst[i] = v; });
+  if (a.splits == 1) {
+    for_each_output([&](int64_t i, int col, float v) { store_output(a.epi, a.out, i, col, v); });
+  } else {
+    float* dst = a.partial + split * static_cast<int64_t>(a.M) * a.N;
+    for_each_output([&](int64_t i, int, float v) { dst[i] = v; });
+  }
 }
 
 template <int BITS, typename PT>
@@ -334,6 +338,7 @@ hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
   a.b = p.b;
   a.bs0 = p.bs0;
   a.out = p.out;
+  a.epi = p.epi;
   a.M = static_cast<int>(p.M);
   a.N = static_cast<int>(p.N);
   a.K = static_cast<int>(p.K);

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QmmProblem p, int ksplit) {
       for (int r = 0; r < kRows; ++r)
 #pragma unroll
         for (int m = 0; m < MR; ++m)
-          if (n0 + r < p.N && m0 + m < p.M) p.out[(m0 + m) * p.N + n0 + r] = y[r][m];
+          if (n0 + r < p.N && m0 + m < p.M) store_output(p.epi, p.out, (m0 + m) * p.N + n0 + r, n0 + r, y[r][m]);
     }
     return;
   }
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QmmProblem p, int ksplit) {
     const int m = lane % MR;
     float v = 0.0f;
     for (int j = 0; j < ksplit; ++j) v += partial[wave + j][r][m];
-    if (n0 + r < p.N && m0 + m < p.M) p.out[(m0 + m) * p.N + n0 + r] = v;
+    if (n0 + r < p.N && m0 + m < p.M) store_output(p.epi, p.out, (m0 + m) * p.N + n0 + r, n0 + r, v);
   }
 }
 
@@ -278,8 +278,17 @@ bool gemv1_supports(const QmmProblem& p) {
   return lds <= static_cast<size_t>(gemv1::kMaxLdsBytes);
 }
 
+bool gemv_pair_supports(const QmmProblem& p) {
+  // The second projection has the first one's shapes and strides (checked
+  // by the caller); its pointers need the same alignment.
+  const int pbytes = p.p_dtype == AFFON_ROCM_BF16 ? 2 : 4;
+  return gemv1_supports(p) && reinterpret_cast<uintptr_t>(p.epi.w2) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(p.epi.s2) % pbytes == 0 && reinterpret_cast<uintptr_t>(p.epi.b2) % pbytes == 0;
+}
+
 hipError_t gemv_launch(const QmmProblem& p, const Launch& l) {
   hipStream_t stream = l.stream;
+  if (p.epi.kind == kEpiSiluPair && !gemv_pair_supports(p)) return hipErrorInvalidValue;
   if (gemv1_supports(p)) {
     switch (p.bits) {
       case 2: return gemv1_launch_b2(p, stream);

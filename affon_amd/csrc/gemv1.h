@@ -19,7 +19,11 @@
 //     (bf16 x) or v_fma_f32 (f32 x); each chunk lies inside one group, so its
 //     parameters are applied once per chunk: y += s * sum(x*q) + b * sum(x);
 //   * rows are reduced across the wave with butterfly shuffles and across the
-//     K-parts of a workgroup through LDS.
+//     K-parts of a workgroup through LDS;
+//   * with PAIR, the wave's first R/2 rows are rows of a gate projection and
+//     the last R/2 the same rows of an up projection (same activations, same
+//     strides), and the wave stores silu(gate) * up: the SiLU-gated
+//     feed-forward input in one pass over both weight matrices.
 #pragma once
 
 #include "device.h"
@@ -48,6 +52,7 @@ struct Args {
   int chunks;  // 16-byte chunks per row
   int part;    // chunks per K-part
   int ks;      // K-parts per row (waves per row block)
+  Epilogue epi;
 };
 
 template <int BITS>
@@ -321,8 +326,10 @@ __device__ __forceinline__ void stage_pieces(u32x4_t v, int p, int count, uint4*
   }
 }
 
-template <int BITS, typename XT, typename PT, int R, int CPL>
+template <int BITS, typename XT, typename PT, int R, int CPL, bool PAIR>
 __global__ __launch_bounds__(kThreads) void kernel(Args a) {
+  static_assert(!PAIR || R % 2 == 0, "paired rows");
+  constexpr int RO = PAIR ? R / 2 : R;  // output rows per wave
   using XS = XStage<BITS, XT>;
   constexpr int XDW = XS::kDwords;
   extern __shared__ uint32_t smem[];
@@ -336,10 +343,16 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int kp = wave % a.ks;
-  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * R;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * RO;
   const int c_begin = kp * a.part;
   const int c_end = min(a.chunks, c_begin + a.part);
-  auto clamp_row = [&](int64_t n) { return n < a.N ? n : a.N - 1; };
+  // Row r of the wave: output row n0 + r % RO of the first (r < RO) or the
+  // second projection.
+  auto row_of = [&](int r) {
+    const int64_t n = n0 + (r % RO);
+    return n < a.N ? n : a.N - 1;
+  };
+  auto second = [](int r) { return PAIR && r >= RO; };
 
   // 1. Loads, in the order their data is needed (the load counter drains in
   //    order): the activation pieces this thread stages, the group parameters
@@ -364,9 +377,9 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     const uint32_t goff = static_cast<uint32_t>((c < c_end ? c : 0) >> a.cpg_shift) * PT::bytes;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t n = clamp_row(n0 + r);
-      const uint8_t* srow = a.s + n * a.ss0 * PT::bytes;
-      const uint8_t* brow = a.b + n * a.bs0 * PT::bytes;
+      const int64_t n = row_of(r);
+      const uint8_t* srow = (second(r) ? a.epi.s2 : a.s) + n * a.ss0 * PT::bytes;
+      const uint8_t* brow = (second(r) ? a.epi.b2 : a.b) + n * a.bs0 * PT::bytes;
       if constexpr (PT::bytes == 2) {
         sraw[r][i] = *reinterpret_cast<const uint16_t*>(srow + goff);
         braw[r][i] = *reinterpret_cast<const uint16_t*>(brow + goff);
@@ -381,8 +394,8 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   uint32_t wv[R][CPL][4];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t n = clamp_row(n0 + r);
-    const u32x4_t* row = reinterpret_cast<const u32x4_t*>(a.w + n * a.ws0);
+    const int64_t n = row_of(r);
+    const u32x4_t* row = reinterpret_cast<const u32x4_t*>((second(r) ? a.epi.w2 : a.w) + n * a.ws0);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = c_begin + lane + 64 * i;
@@ -449,12 +462,23 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) y[r] = tot[r];
   }
+  // Lane o < RO stores output row n0 + o.
+  auto finish = [&](float v, float up) {
+    if (n0 + lane >= a.N) return;
+    if constexpr (PAIR)
+      a.out[n0 + lane] = silu(v) * up;
+    else
+      store_output(a.epi, a.out, n0 + lane, n0 + lane, v);
+  };
   if (a.ks == 1) {
-    if (lane < R) {
-      float v = y[0];
+    if (lane < RO) {
+      float v = y[0], up = y[RO % R];
 #pragma unroll
-      for (int r = 1; r < R; ++r) v = lane == r ? y[r] : v;
-      if (n0 + lane < a.N) a.out[n0 + lane] = v;
+      for (int r = 1; r < RO; ++r) {
+        v = lane == r ? y[r] : v;
+        up = lane == r ? y[(r + RO) % R] : up;
+      }
+      finish(v, up);
     }
     return;
   }
@@ -463,20 +487,24 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     for (int r = 0; r < R; ++r) red[wave * R + r] = y[r];
   }
   __syncthreads();
-  if (kp == 0 && lane < R) {
-    float v = 0.0f;
-    for (int j = 0; j < a.ks; ++j) v += red[(wave + j) * R + lane];
-    if (n0 + lane < a.N) a.out[n0 + lane] = v;
+  if (kp == 0 && lane < RO) {
+    float v = 0.0f, up = 0.0f;
+    for (int j = 0; j < a.ks; ++j) {
+      v += red[(wave + j) * R + lane];
+      if constexpr (PAIR) up += red[(wave + j) * R + RO + lane];
+    }
+    finish(v, up);
   }
 }
 
-template <int BITS, typename XT, typename PT, int R, int CPL>
+template <int BITS, typename XT, typename PT, int R, int CPL, bool PAIR>
 hipError_t launch(const Args& a, hipStream_t stream) {
+  constexpr int RO = PAIR ? R / 2 : R;
   const size_t lds = lds_size<BITS, XT, R>(a.chunks);
-  const int64_t row_blocks = (a.N + R - 1) / R;
+  const int64_t row_blocks = (a.N + RO - 1) / RO;
   const int64_t per_block = kWaves / a.ks;
   const unsigned blocks = static_cast<unsigned>((row_blocks + per_block - 1) / per_block);
-  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL>), dim3(blocks), dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL, PAIR>), dim3(blocks), dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
 

@@ -8,6 +8,8 @@
 // picks the fastest variant, or one within 3% of it, on each of 8-bit
 // 14336x4096 and 4096x14336, 4-bit 14336x4096, 4096x14336, 4096x4096,
 // 1024x4096 and 128256x4096 (bf16), and 4-bit 4096x4096 with f32 operands.
+// Paired gate/up problems choose among the even-R variants the same way,
+// counting R/2 output rows per wave.
 #pragma once
 
 #include <map>
@@ -36,20 +38,32 @@ size_t lds_bytes(int chunks) {
   return lds_size<BITS, XT, R>(chunks);
 }
 
-template <int BITS, typename XT, typename PT>
+#define AFFON_GEMV1_VARIANT(R, CPL, PAIR)                                            \
+  {R, CPL, launch<BITS, XT, PT, R, CPL, PAIR>,                                        \
+   reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL, PAIR>), lds_bytes<BITS, XT, R>}
+
+template <int BITS, typename XT, typename PT, bool PAIR>
 const Variant* variants(int* count) {
-#define AFFON_GEMV1_VARIANT(R, CPL)                                                                   \
-  {R, CPL, launch<BITS, XT, PT, R, CPL>, reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL>), \
-   lds_bytes<BITS, XT, R>}
-  static const Variant table[] = {
-      AFFON_GEMV1_VARIANT(1, 1), AFFON_GEMV1_VARIANT(2, 1), AFFON_GEMV1_VARIANT(4, 1), AFFON_GEMV1_VARIANT(8, 1),
-      AFFON_GEMV1_VARIANT(1, 2), AFFON_GEMV1_VARIANT(2, 2), AFFON_GEMV1_VARIANT(4, 2), AFFON_GEMV1_VARIANT(1, 4),
-      AFFON_GEMV1_VARIANT(2, 4), AFFON_GEMV1_VARIANT(4, 4),
-  };
-#undef AFFON_GEMV1_VARIANT
-  *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
-  return table;
+  if constexpr (PAIR) {
+    static const Variant table[] = {
+        AFFON_GEMV1_VARIANT(2, 1, true), AFFON_GEMV1_VARIANT(4, 1, true), AFFON_GEMV1_VARIANT(8, 1, true),
+        AFFON_GEMV1_VARIANT(2, 2, true), AFFON_GEMV1_VARIANT(4, 2, true), AFFON_GEMV1_VARIANT(2, 4, true),
+        AFFON_GEMV1_VARIANT(4, 4, true),
+    };
+    *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
+    return table;
+  } else {
+    static const Variant table[] = {
+        AFFON_GEMV1_VARIANT(1, 1, false), AFFON_GEMV1_VARIANT(2, 1, false), AFFON_GEMV1_VARIANT(4, 1, false),
+        AFFON_GEMV1_VARIANT(8, 1, false), AFFON_GEMV1_VARIANT(1, 2, false), AFFON_GEMV1_VARIANT(2, 2, false),
+        AFFON_GEMV1_VARIANT(4, 2, false), AFFON_GEMV1_VARIANT(1, 4, false), AFFON_GEMV1_VARIANT(2, 4, false),
+        AFFON_GEMV1_VARIANT(4, 4, false),
+    };
+    *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
+    return table;
+  }
 }
+#undef AFFON_GEMV1_VARIANT
 
 inline int device_cus() {
   static std::mutex mutex;
@@ -80,7 +94,7 @@ inline int blocks_per_cu(const void* fn, size_t lds) {
   return blocks;
 }
 
-template <int BITS, typename XT, typename PT>
+template <int BITS, typename XT, typename PT, bool PAIR>
 hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
   Args a;
   a.w = p.w;
@@ -91,12 +105,13 @@ hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
   a.bs0 = p.bs0;
   a.x = p.x;
   a.out = p.out;
+  a.epi = p.epi;
   a.N = p.N;
   a.chunks = static_cast<int>(p.K * BITS / 128);
   a.cpg_shift = 0;
   while ((int64_t(1) << a.cpg_shift) * chunk_values<BITS>() < p.group) ++a.cpg_shift;
   int count = 0;
-  const Variant* table = variants<BITS, XT, PT>(&count);
+  const Variant* table = variants<BITS, XT, PT, PAIR>(&count);
   const int cus = device_cus();
   const Variant* best = nullptr;
   int best_ks = 0;
@@ -111,7 +126,8 @@ hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
     const size_t lds = v.lds(a.chunks);
     if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
     const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
-    const int64_t waves = (p.N + v.R - 1) / v.R * ks;
+    const int rows_out = PAIR ? v.R / 2 : v.R;
+    const int64_t waves = (p.N + rows_out - 1) / rows_out * ks;
     const int64_t rounds = (waves + capacity - 1) / capacity;
     const bool better = best == nullptr || rounds < best_rounds ||
                         (rounds == best_rounds && (ks < best_ks || (ks == best_ks && waves > best_waves)));
@@ -128,14 +144,20 @@ hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
   return best->launch(a, stream);
 }
 
+template <int BITS, bool PAIR>
+hipError_t dispatch_pair(const QmmProblem& p, hipStream_t stream) {
+  if (p.x_dtype == AFFON_ROCM_BF16) {
+    if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, BF16, BF16, PAIR>(p, stream);
+    return dispatch<BITS, BF16, F32, PAIR>(p, stream);
+  }
+  if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, F32, BF16, PAIR>(p, stream);
+  return dispatch<BITS, F32, F32, PAIR>(p, stream);
+}
+
 template <int BITS>
 hipError_t dispatch_bits(const QmmProblem& p, hipStream_t stream) {
-  if (p.x_dtype == AFFON_ROCM_BF16) {
-    if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, BF16, BF16>(p, stream);
-    return dispatch<BITS, BF16, F32>(p, stream);
-  }
-  if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, F32, BF16>(p, stream);
-  return dispatch<BITS, F32, F32>(p, stream);
+  if (p.epi.kind == kEpiSiluPair) return dispatch_pair<BITS, true>(p, stream);
+  return dispatch_pair<BITS, false>(p, stream);
 }
 
 }  // namespace gemv1

@@ -264,7 +264,11 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
     const int row = o / kCols, col = n0 + o % kCols;
     if (row < a.M && col < a.N) {
       const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
-      dst[static_cast<int64_t>(row) * a.N + col] = v;
+      const int64_t i = static_cast<int64_t>(row) * a.N + col;
+      if (a.splits == 1)
+        store_output(a.epi, dst, i, col, v);
+      else
+        dst[i] = v;
     }
   }
 }
@@ -338,6 +342,7 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
   a.b = p.b;
   a.bs0 = p.bs0;
   a.out = p.out;
+  a.epi = p.epi;
   a.M = static_cast<int>(p.M);
   a.N = static_cast<int>(p.N);
   a.K = static_cast<int>(p.K);

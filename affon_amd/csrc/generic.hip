@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256) void qmm_generic_kernel(QmmProblem p) {
     const float w = s * static_cast<float>(q) + b;
     acc = acc + XT::load(xrow, k * p.xs1) * w;
   }
-  p.out[m * p.N + n] = acc;
+  store_output(p.epi, p.out, m * p.N + n, n, acc);
 }
 
 template <typename XT>

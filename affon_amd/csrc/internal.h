@@ -5,6 +5,7 @@
 #include <cstdint>
 
 #include "affon_rocm.h"
+#include "epilogue.h"
 
 namespace affon {
 
@@ -25,6 +26,7 @@ struct QmmProblem {
   int64_t bs0 = 0, bs1 = 0;
   int p_dtype = AFFON_ROCM_F32;
   float* out = nullptr;
+  Epilogue epi;  // applied by the kernel that stores each output element
 };
 
 // Device scratch memory owned by a session and ordered by its stream.
@@ -58,6 +60,9 @@ bool generic_supports(const QmmProblem& p);
 hipError_t generic_launch(const QmmProblem& p, const Launch& l);
 
 bool gemv_supports(const QmmProblem& p);
+// Whether the gemv candidate computes a kSiluPair problem (both projections)
+// in one launch.
+bool gemv_pair_supports(const QmmProblem& p);
 hipError_t gemv_launch(const QmmProblem& p, const Launch& l);
 
 bool gemv_mfma_supports(const QmmProblem& p);

@@ -43,6 +43,7 @@ struct TileArgs {
   // and reduce_partials_kernel forms the output.
   int splits, split_steps;
   float* partial;
+  Epilogue epi;  // applied where the output is stored (the reduction when splits > 1)
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {

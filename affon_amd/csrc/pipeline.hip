@@ -7,21 +7,28 @@ namespace pipeline {
 namespace {
 
 // out[i] = sum of the K ranges' partial sums, added in range order (the same
-// result on every run). Four outputs per thread; `count` = M*N; `vec` when
-// count % 4 == 0 and out is 16-byte aligned (partial always is).
+// result on every run), then the output epilogue. Four outputs per thread;
+// `count` = M*N, `n` = N; `vec` when count % 4 == 0 and out is 16-byte
+// aligned (partial always is).
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* partial, float* out, int64_t count,
-                                                              int splits, int vec) {
+                                                              int64_t n, int splits, int vec, Epilogue epi) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i >= count) return;
   if (vec) {
     f32x4_t sum = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + i));
     for (int r = 1; r < splits; ++r) sum += __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + r * count + i));
-    *reinterpret_cast<f32x4_t*>(out + i) = sum;
+    if (epi.kind == kEpiNone) {
+      *reinterpret_cast<f32x4_t*>(out + i) = sum;
+    } else {
+      const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) store_output(epi, out, i + k, (i + k) % n, v[k]);
+    }
   } else {
     for (int64_t j = i; j < i + 4 && j < count; ++j) {
       float sum = partial[j];
       for (int r = 1; r < splits; ++r) sum += partial[r * count + j];
-      out[j] = sum;
+      store_output(epi, out, j, j % n, sum);
     }
   }
 }
@@ -61,7 +68,7 @@ hipError_t launch_reduce(const TileArgs& args, hipStream_t stream) {
   const int64_t blocks = (count + 1023) / 1024;
   const int vec = count % 4 == 0 && reinterpret_cast<uintptr_t>(args.out) % 16 == 0;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     args.partial, args.out, count, args.splits, vec);
+                     args.partial, args.out, count, static_cast<int64_t>(args.N), args.splits, vec, args.epi);
   return hipGetLastError();
 }
 

@@ -66,6 +66,7 @@ struct Args {
   int part;          // sets per K-part (the variant's CPL)
   int ks;            // K-parts per row block (waves per row block)
   int groups;        // groups per row
+  Epilogue epi;
 };
 
 template <int BITS>
@@ -333,7 +334,8 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   for (int j = 0; j < NV; ++j) {
     const int m = (j * (4 / NV) + 4 * (q >> 1)) >> LE;
     if (a.ks == 1) {
-      if (writer && m < a.M && n0 + r < a.N) a.out[static_cast<int64_t>(m) * a.N + n0 + r] = v[j];
+      if (writer && m < a.M && n0 + r < a.N)
+        store_output(a.epi, a.out, static_cast<int64_t>(m) * a.N + n0 + r, n0 + r, v[j]);
     } else if (writer && m < a.M) {
       red[(wave * MP + m) * kRows + r] = v[j];
     }
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     if (kp == 0 && writer && m < a.M && n0 + r < a.N) {
       float t = 0.0f;
       for (int k = 0; k < a.ks; ++k) t += red[((wave + k) * MP + m) * kRows + r];
-      a.out[static_cast<int64_t>(m) * a.N + n0 + r] = t;
+      store_output(a.epi, a.out, static_cast<int64_t>(m) * a.N + n0 + r, n0 + r, t);
     }
   }
 }

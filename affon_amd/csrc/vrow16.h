@@ -60,6 +60,7 @@ struct Args {
   int part;          // sets per K-part (the variant's CPL)
   int ks;            // K-parts per row block (waves per row block)
   int groups;        // groups per row
+  Epilogue epi;
 };
 
 template <int BITS>
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
   const bool writer = (q % (4 / MP)) == 0 && m_d < a.M;
   if (a.ks == 1) {
-    if (writer && n0 + n < a.N) a.out[static_cast<int64_t>(m_d) * a.N + n0 + n] = v;
+    if (writer && n0 + n < a.N) store_output(a.epi, a.out, static_cast<int64_t>(m_d) * a.N + n0 + n, n0 + n, v);
     return;
   }
   if (writer) red[(wave * MP + m_d) * kRows + n] = v;
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   if (kp == 0 && writer && n0 + n < a.N) {
     float t = 0.0f;
     for (int j = 0; j < a.ks; ++j) t += red[((wave + j) * MP + m_d) * kRows + n];
-    a.out[static_cast<int64_t>(m_d) * a.N + n0 + n] = t;
+    store_output(a.epi, a.out, static_cast<int64_t>(m_d) * a.N + n0 + n, n0 + n, t);
   }
 }
 

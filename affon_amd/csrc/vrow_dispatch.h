@@ -117,6 +117,7 @@ hipError_t dispatch_pt(const QmmProblem& p, hipStream_t stream) {
   a.b = p.b;
   a.bs0 = p.bs0;
   a.out = p.out;
+  a.epi = p.epi;
   a.M = static_cast<int>(p.M);
   a.N = static_cast<int>(p.N);
   a.K = static_cast<int>(p.K);

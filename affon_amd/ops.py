@@ -126,6 +126,103 @@ def quantized_matmul_into(out: Tensor, input: Tensor, packed: Tensor, scales: Te
                                  implementation=implementation, out=out)
 
 
+# ---- fused output epilogues ------------------------------------------------
+# The reference authors a linear layer's output bias and the SiLU-gated
+# feed-forward product as separate ops after quantized_matmul
+# (docs/core/quantized-inference.md:37-42, packages/@affon/models/src/llama/
+# model.ts:82); these run them in the kernel that stores the output.
+
+def _check_triple(name: str, triple: Any) -> tuple[Tensor, Tensor, Tensor]:
+    if not isinstance(triple, (tuple, list)) or len(triple) != 3 or not all(isinstance(t, Tensor) for t in triple):
+        raise TypeError(f"{name} must be a (packed, scales, biases) tuple of tensors")
+    return tuple(triple)  # type: ignore[return-value]
+
+
+def _epilogue(output_bias: Tensor | None = None, up: tuple[Tensor, Tensor, Tensor] | None = None) -> _native.Epilogue:
+    epi = _native.Epilogue()
+    epi.kind = _native.EPILOGUE_NONE
+    if output_bias is not None:
+        epi.kind = _native.EPILOGUE_BIAS
+        epi.bias = output_bias.data_ptr
+        epi.bias_bytes = output_bias._buffer.nbytes - output_bias.offset * (2 if output_bias.dtype == "bf16" else 4)
+        epi.bias_dtype = {"f32": _native.F32, "bf16": _native.BF16}.get(output_bias.dtype, -1)
+    if up is not None:
+        epi.kind = _native.EPILOGUE_SILU_GATE
+        epi.up_packed, epi.up_scales, epi.up_biases = (t.view() for t in up)
+    return epi
+
+
+def _check_bias(bias: Tensor, outputs: int) -> None:
+    if bias.dtype not in ("f32", "bf16") or len(bias.shape) != 1 or bias.shape[0] != outputs or not bias.is_contiguous():
+        raise TypeError("quantized_matmul output bias must be a contiguous f32/bf16 [N] tensor")
+
+
+def _run_fused(x: Tensor, w: Tensor, s: Tensor, b: Tensor, bits: int, group: int, epi: _native.Epilogue, *,
+               policy: str, implementation: str, out: Tensor | None) -> Tensor:
+    session = x.session
+    if out is None:
+        out = session.empty("f32", (x.shape[0], w.shape[0]))
+    elif out.dtype != "f32" or out.shape != (x.shape[0], w.shape[0]) or not out.is_contiguous():
+        raise TypeError("quantized_matmul output must be a contiguous f32 [M,N] tensor")
+    desc = _descriptor(x, w, s, b, bits, group, out, implementation, policy)
+    _native.check(_native.load().affon_rocm_quantized_matmul_fused(session._handle, ctypes.byref(desc),
+                                                                    ctypes.byref(epi)), "Program execution failed")
+    return out
+
+
+def quantized_linear(input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, output_bias: Tensor, *,
+                     bits: int, group_size: int, implementation: str = "auto", policy: str = "backend_equivalent",
+                     out: Tensor | None = None) -> Tensor:
+    """``add(quantized_matmul(input, packed, scales, biases), output_bias)`` in
+    one launch: Y[m,n] = qmm[m,n] + output_bias[n] (one f32 add, the same
+    rounding as the separate ``add``)."""
+    operands = (input, packed, scales, biases, output_bias)
+    if not all(isinstance(o, Tensor) for o in operands):
+        raise TypeError("quantized_linear requires evaluated tensors")
+    if any(o.session is not input.session for o in operands):
+        raise TypeError("quantized_linear operands must belong to the same Session")
+    _validate([t.spec for t in operands[:4]], {"bits": bits, "group_size": group_size})
+    _check_bias(output_bias, packed.shape[0])
+    return _run_fused(input, packed, scales, biases, bits, group_size, _epilogue(output_bias=output_bias),
+                      policy=policy, implementation=implementation, out=out)
+
+
+def quantized_silu_gate(input: Tensor, gate: Any, up: Any, *, bits: int, group_size: int,
+                        implementation: str = "auto", policy: str = "backend_equivalent",
+                        out: Tensor | None = None) -> Tensor:
+    """``mul(silu(quantized_matmul(input, *gate)), quantized_matmul(input, *up))``:
+    the SiLU-gated feed-forward input. ``gate`` and ``up`` are (packed, scales,
+    biases) tuples of the same shapes and dtypes. Runs in one launch where the
+    selected kernel pairs rows of both projections (M = 1), else in two, the
+    second storing silu(gate) * up."""
+    gate = _check_triple("gate", gate)
+    up = _check_triple("up", up)
+    operands = (input, *gate, *up)
+    if any(o.session is not input.session for o in operands):
+        raise TypeError("quantized_silu_gate operands must belong to the same Session")
+    _validate([t.spec for t in (input, *gate)], {"bits": bits, "group_size": group_size})
+    _validate([t.spec for t in (input, *up)], {"bits": bits, "group_size": group_size})
+    if tuple(t.spec for t in gate) != tuple(t.spec for t in up):
+        raise TypeError("quantized_silu_gate gate and up projections must have the same shapes and dtypes")
+    return _run_fused(input, *gate, bits, group_size, _epilogue(up=up), policy=policy,
+                      implementation=implementation, out=out)
+
+
+def fused_plan(input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, *, bits: int, group_size: int,
+               output_bias: Tensor | None = None, up: Any = None, implementation: str = "auto",
+               policy: str = "backend_equivalent") -> str:
+    """The launches a fused call makes: implementation ids with the epilogue
+    in brackets, separated by ';'."""
+    desc = _descriptor(input, packed, scales, biases, bits, group_size, None, implementation, policy)
+    desc.output = 1
+    desc.output_bytes = input.shape[0] * packed.shape[0] * 4
+    epi = _epilogue(output_bias=output_bias, up=_check_triple("up", up) if up is not None else None)
+    name = ctypes.create_string_buffer(256)
+    _native.check(_native.load().affon_rocm_quantized_matmul_fused_select(ctypes.byref(desc), ctypes.byref(epi),
+                                                                           name, 256), "select")
+    return name.value.decode()
+
+
 def selected_implementation(input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, *, bits: int,
                             group_size: int, implementation: str = "auto",
                             policy: str = "backend_equivalent") -> str:

@@ -130,6 +130,48 @@ int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qm
  * (src/js/compute/native.zig:1314-1322). */
 int affon_rocm_quantized_matmul_select(const affon_rocm_qmm_desc* desc, char* id, size_t cap);
 
+/* ---- fused output epilogues (no reference counterpart: the reference
+ *      authors a linear layer's output bias and the SiLU-gated feed-forward
+ *      product as separate ops after quantized_matmul,
+ *      docs/core/quantized-inference.md:37-42 `add(projected, output_bias)` and
+ *      packages/@affon/models/src/llama/model.ts:82
+ *      `mul(silu(matmul(h, gate)), matmul(h, up))`) ---- */
+enum {
+  AFFON_ROCM_EPILOGUE_NONE = 0,      /* plain quantized_matmul */
+  AFFON_ROCM_EPILOGUE_BIAS = 1,      /* output[m,n] = qmm[m,n] + bias[n], one f32 add */
+  AFFON_ROCM_EPILOGUE_SILU_GATE = 2  /* output[m,n] = silu(gate[m,n]) * up[m,n], silu(g) = g / (1 + e^-g) */
+};
+
+typedef struct {
+  int32_t kind;           /* AFFON_ROCM_EPILOGUE_* */
+  /* BIAS: N contiguous f32 | bf16 device elements, element-aligned. */
+  const void* bias;
+  size_t bias_bytes;
+  int32_t bias_dtype;
+  /* SILU_GATE: the up projection. The descriptor's packed/scales/biases are
+   * the gate projection; these views have the same shapes and dtypes. */
+  affon_rocm_view up_packed;
+  affon_rocm_view up_scales;
+  affon_rocm_view up_biases;
+} affon_rocm_qmm_epilogue;
+
+/* quantized_matmul with an output epilogue applied by the kernel that stores
+ * each output element. Validation and implementation selection are those of
+ * affon_rocm_quantized_matmul (plus the epilogue's operands); implementation
+ * and numerical_policy apply to every launch. SILU_GATE runs as one launch
+ * when the selected kernel computes rows of both projections together (the
+ * M = 1 gemv kernel, with equal strides), otherwise as two launches: the gate
+ * projection into output, then the up projection, whose kernel stores
+ * silu(output) * up. */
+int affon_rocm_quantized_matmul_fused(affon_rocm_session* session, const affon_rocm_qmm_desc* desc,
+                                      const affon_rocm_qmm_epilogue* epilogue);
+
+/* Plan of a fused call: the implementation id of each launch with its
+ * epilogue in brackets, launches separated by ';'
+ * (e.g. "rocm_quantized_matmul.gemv[silu_gate]"). */
+int affon_rocm_quantized_matmul_fused_select(const affon_rocm_qmm_desc* desc, const affon_rocm_qmm_epilogue* epilogue,
+                                             char* id, size_t cap);
+
 /* JSON array describing every registered candidate: id, version, numerical
  * class and guard (capability registration for the rocm backend). */
 const char* affon_rocm_quantized_matmul_capabilities(void);

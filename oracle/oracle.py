@@ -133,3 +133,30 @@ def dequantize(packed: np.ndarray, scales: np.ndarray, biases: np.ndarray, bits:
     load().oracle_dequantize(packed.ctypes.data, scales.ctypes.data, biases.ctypes.data, _code(scales), N, K, bits,
                              group_size, BF16 if out_dtype == "bf16" else F32, out.ctypes.data)
     return out
+
+
+# ---- the element-wise ops the reference applies after quantized_matmul ----
+
+def add_output_bias(y: np.ndarray, bias: np.ndarray) -> np.ndarray:
+    """``add(projected, output_bias)`` (docs/core/quantized-inference.md:37-42):
+    one f32 add per element, bias broadcast over rows (bf16 bias widened
+    exactly). Pinned in tests/test_oracle.py by exact dyadic sums and the zero
+    bias identity."""
+    b = f32_from_bf16(bias) if bias.dtype == np.uint16 else np.asarray(bias, dtype=np.float32)
+    return (np.asarray(y, dtype=np.float32) + b[None, :]).astype(np.float32)
+
+
+def silu(g: np.ndarray) -> np.ndarray:
+    """f32 ``silu(g) = g * sigmoid(g)`` written g / (1 + e^-g)
+    (packages/@affon/models/src/llama/model.ts:82 applies ``silu`` to the gate
+    projection). Pinned in tests/test_oracle.py by silu(0) = 0, the limits
+    silu(g) -> g and -> 0, the odd-part identity silu(g) - silu(-g) = g, and
+    an f64 evaluation of g * sigmoid(g) (within 4 ulp)."""
+    g = np.asarray(g, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (g / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
+
+
+def silu_gate(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """``mul(silu(gate), up)`` in f32 (model.ts:82)."""
+    return (silu(gate) * np.asarray(up, dtype=np.float32)).astype(np.float32)

@@ -341,3 +341,38 @@ def test_product_generator_matches_oracle_generator():
     for seed, count, mean, std in [(1, 4097, 0.0, 1.0), (2, 10_001, 0.0, 0.02), (20261105, 3, 0.5, 2.0)]:
         expected, _ = O.randn(seed, count, mean, std)
         np.testing.assert_array_equal(normal_f32(seed, count, mean, std), expected)
+
+
+# ---- element-wise epilogue ops (add of the output bias, silu gate) ----
+
+def test_add_output_bias_exact_dyadic(rng):
+    """Dyadic values with few significant bits add exactly in f32, so the sum
+    is fixed; a zero bias is the identity; a bf16 bias is widened exactly."""
+    y = rng.integers(-64, 64, size=(3, 10)) / 8.0
+    bias = rng.integers(-16, 16, size=10) / 4.0
+    got = O.add_output_bias(y.astype(np.float32), bias.astype(np.float32))
+    np.testing.assert_array_equal(got, (y + bias[None, :]).astype(np.float32))
+    np.testing.assert_array_equal(O.add_output_bias(y.astype(np.float32), O.bf16_from_f32(bias.astype(np.float32))),
+                                  got)
+    yr = rng.standard_normal((2, 5)).astype(np.float32)
+    np.testing.assert_array_equal(O.add_output_bias(yr, np.zeros(5, np.float32)), yr)
+
+
+def test_silu_closed_forms_and_identities(rng):
+    """silu(0) = 0; silu(g) -> g for large g and -> 0 (from below) for very
+    negative g; silu(g) - silu(-g) = g (the odd part of g * sigmoid(g));
+    within 4 ulp of g * sigmoid(g) evaluated in f64 (exp, add and divide
+    each round)."""
+    assert O.silu(np.float32(0.0)) == 0.0
+    big = np.array([30.0, 60.0, 88.0], np.float32)
+    np.testing.assert_array_equal(O.silu(big), big)
+    tiny = O.silu(np.array([-100.0, -200.0], np.float32))
+    assert np.all(tiny <= 0) and np.all(tiny > -1e-30)
+    g = (rng.standard_normal(4096) * 4).astype(np.float32)
+    odd = O.silu(g).astype(np.float64) - O.silu(-g).astype(np.float64)
+    assert np.all(np.abs(odd - g) <= 2e-6 * np.maximum(1.0, np.abs(g)))
+    exact = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(O.silu(g) - exact) <= 4 * ulp + 1e-45)
+    up = rng.standard_normal(4096).astype(np.float32)
+    np.testing.assert_array_equal(O.silu_gate(g, up), (O.silu(g) * up).astype(np.float32))
