@@ -11,8 +11,10 @@ linear path touches:
   slice) share storage and carry element strides and a byte offset
   (docs/core/quantized-inference.md:47-49);
 * ``TensorSpec`` / ``program`` / ``Executable`` author and run a formal
-  Program with one ``quantized_matmul`` node (src/js/compute/program.ts:481-494,
-  1856-1885, 1704-1737).
+  Program of ``quantized_matmul`` nodes (src/js/compute/program.ts:481-494,
+  1856-1885, 1704-1737), with one or several outputs; ``add`` / ``mul`` /
+  ``silu`` nodes after them are lowered into the kernels' output epilogues
+  (lowering.py).
 
 Device memory comes from the native library; there is no CPU execution path.
 """
@@ -326,47 +328,57 @@ class ProgramBuilder:
 class Program:
     name: str
     nodes: list[dict[str, Any]]
-    output: int
+    outputs: list[int]
+    multiple: bool = False  # the body returned a sequence of outputs
+
+    @property
+    def output(self) -> int:
+        return self.outputs[0]
 
     def inspect(self) -> dict[str, Any]:
-        return {"name": self.name, "nodes": [dict(n) for n in self.nodes], "outputs": [self.output]}
+        return {"name": self.name, "nodes": [dict(n) for n in self.nodes], "outputs": list(self.outputs)}
 
 
-def program(name: str, fn: Callable[[ProgramBuilder], FormalTensor]) -> Program:
+def program(name: str, fn: Callable[[ProgramBuilder], Any]) -> Program:
+    """Authors a Program; the body returns one formal tensor or a sequence of
+    them (src/js/compute/program.ts:1704-1737: Programs may return several
+    outputs)."""
     builder = ProgramBuilder(name)
     result = fn(builder)
-    if not isinstance(result, FormalTensor) or result.builder is not builder:
-        raise TypeError("program body must return a formal tensor of the same Program")
-    return Program(name, builder.nodes, result.node)
+    multiple = isinstance(result, (list, tuple))
+    results = list(result) if multiple else [result]
+    if not results or any(not isinstance(r, FormalTensor) or r.builder is not builder for r in results):
+        raise TypeError("program body must return formal tensors of the same Program")
+    return Program(name, builder.nodes, [r.node for r in results], multiple)
 
 
 class Executable:
     """A compiled Program: validated once, run with named arguments."""
 
     def __init__(self, session: Session, source: Program, options: dict[str, str]):
-        from . import ops  # local: ops imports core
+        from . import lowering, ops  # local: ops imports core
         self.session = session
         self.program = source
         self.options = options
         self._ops = ops
-        self._plan = []
-        for node in source.nodes:
-            if node["kind"] != "operation":
-                continue
-            if node["op"] != "quantized_matmul":
-                raise TypeError(f"unsupported operation on rocm: {node['op']}")
-            self._plan.append(node)
+        self._steps = lowering.lower(source.nodes, source.outputs)
         # Selection happens at compile time from the formal specs, so an
         # unsupported policy fails here as in the reference compiler.
-        self._implementations = [self._select(node) for node in self._plan]
+        self._implementations = [self._select(step) for step in self._steps]
 
-    def _select(self, node: dict[str, Any]) -> str:
-        specs = [self.program.nodes[i]["spec"] for i in node["operands"]]
-        return self._ops.select_for_specs(specs, node["options"], self.options["numericalPolicy"])
+    def _select(self, step: Any) -> str:
+        specs = [self.program.nodes[i]["spec"] for i in step.operands]
+        policy = self.options["numericalPolicy"]
+        if step.kind == "quantized_matmul":
+            return self._ops.select_for_specs(specs, step.options, policy)
+        return self._ops.fused_select_for_specs(step.kind, specs, step.options, policy)
 
     def explain(self) -> dict[str, Any]:
-        physical = [{"op": node["op"], "implementation_id": impl, "implementation_version": 1,
-                     "options": node["options"]} for node, impl in zip(self._plan, self._implementations)]
+        names = {"quantized_matmul": "quantized_matmul", "bias": "quantized_matmul+add",
+                 "silu_gate": "quantized_matmul+silu+quantized_matmul+mul"}
+        physical = [{"op": names[step.kind], "implementation_id": impl, "implementation_version": 1,
+                     "options": step.options, "nodes": sorted(step.absorbed + [step.node])}
+                    for step, impl in zip(self._steps, self._implementations)]
         return {"program": self.program.name, "device": self.session.device, "options": dict(self.options),
                 "executable": {"physical_nodes": physical}}
 
@@ -382,9 +394,20 @@ class Executable:
                 if value.spec != node["spec"]:
                     raise TypeError(f"argument {node['name']} does not match its spec")
                 values[node["id"]] = value
+        policy = self.options["numericalPolicy"]
+        for step in self._steps:
+            operands = [values[i] for i in step.operands]
+            bits, group = step.options["bits"], step.options["group_size"]
+            if step.kind == "quantized_matmul":
+                values[step.node] = self._ops._run_quantized_matmul(*operands, bits, group, policy=policy)
+            elif step.kind == "bias":
+                self._ops._check_bias(operands[4], operands[1].shape[0])
+                epi = self._ops._epilogue(output_bias=operands[4])
+                values[step.node] = self._ops._run_fused(*operands[:4], bits, group, epi, policy=policy,
+                                                         implementation="auto", out=None)
             else:
-                operands = [values[i] for i in node["operands"]]
-                values[node["id"]] = self._ops._run_quantized_matmul(
-                    *operands, node["options"]["bits"], node["options"]["group_size"],
-                    policy=self.options["numericalPolicy"])
-        return values[self.program.output]
+                epi = self._ops._epilogue(up=tuple(operands[4:7]))
+                values[step.node] = self._ops._run_fused(*operands[:4], bits, group, epi, policy=policy,
+                                                         implementation="auto", out=None)
+        results = [values[i] for i in self.program.outputs]
+        return results if self.program.multiple else results[0]

@@ -15,6 +15,11 @@ packed format.
 
 ``transpose`` and ``slice`` create strided views without copying, as the
 reference's view ops do for evaluated tensors.
+
+``add``, ``mul`` and ``silu`` (src/js/ops.ts:51,53,91) author formal nodes
+only: on the rocm device they run as quantized_matmul output epilogues (an
+output bias, the SiLU-gated product of two projections; see lowering.py),
+and ``quantized_linear`` / ``quantized_silu_gate`` are their evaluated forms.
 """
 from __future__ import annotations
 
@@ -235,18 +240,22 @@ def selected_implementation(input: Tensor, packed: Tensor, scales: Tensor, biase
     return name.value.decode()
 
 
+def _dense_view(spec: TensorSpec, address: int) -> _native.View:
+    """A dense row-major view at an aligned address, as a Program's arguments
+    are when run (selection reads only shapes, strides and alignment)."""
+    rows, cols = spec.shape
+    itemsize = 2 if spec.dtype == "bf16" else 4
+    code = {"f32": _native.F32, "bf16": _native.BF16, "u32": _native.U32}[spec.dtype]
+    return _native.View(address, rows * cols * itemsize, 0, (ctypes.c_int64 * 2)(rows, cols),
+                        (ctypes.c_int64 * 2)(cols, 1), code)
+
+
 def select_for_specs(specs: Sequence[TensorSpec], options: Mapping[str, Any], policy: str) -> str:
     """Compile-time selection from formal specs: dense row-major operands at
     an aligned base, as a Program's arguments are when run."""
     _validate(specs, options)
     desc = _native.QmmDesc()
-    views = []
-    for spec in specs:
-        rows, cols = spec.shape
-        itemsize = 2 if spec.dtype == "bf16" else 4
-        code = {"f32": _native.F32, "bf16": _native.BF16, "u32": _native.U32}[spec.dtype]
-        views.append(_native.View(256, rows * cols * itemsize, 0, (ctypes.c_int64 * 2)(rows, cols),
-                                  (ctypes.c_int64 * 2)(cols, 1), code))
+    views = [_dense_view(spec, 256) for spec in specs]
     desc.input, desc.packed, desc.scales, desc.biases = views
     desc.output = 256
     desc.output_bytes = specs[0].shape[0] * specs[1].shape[0] * 4
@@ -259,6 +268,86 @@ def select_for_specs(specs: Sequence[TensorSpec], options: Mapping[str, Any], po
     if status != _native.OK:
         raise TypeError(f"no rocm quantized_matmul implementation: {_native.last_error()}")
     return name.value.decode()
+
+
+def fused_select_for_specs(kind: str, specs: Sequence[TensorSpec], options: Mapping[str, Any], policy: str) -> str:
+    """Compile-time plan of a fused step from formal specs: ``kind`` "bias"
+    (specs: x, packed, scales, biases, bias) or "silu_gate" (x, gate packed,
+    scales, biases, up packed, scales, biases)."""
+    _validate(specs[:4], options)
+    desc = _native.QmmDesc()
+    desc.input, desc.packed, desc.scales, desc.biases = (_dense_view(spec, 256 * (i + 1))
+                                                         for i, spec in enumerate(specs[:4]))
+    desc.output = 256
+    desc.output_bytes = specs[0].shape[0] * specs[1].shape[0] * 4
+    desc.bits = options["bits"]
+    desc.group_size = options["group_size"]
+    desc.implementation = _native.IMPL_AUTO
+    desc.numerical_policy = policy_code(policy)
+    epi = _native.Epilogue()
+    if kind == "bias":
+        epi.kind = _native.EPILOGUE_BIAS
+        epi.bias = 4096
+        epi.bias_dtype = _native.BF16 if specs[4].dtype == "bf16" else _native.F32
+        epi.bias_bytes = specs[4].shape[0] * (2 if specs[4].dtype == "bf16" else 4)
+    else:
+        epi.kind = _native.EPILOGUE_SILU_GATE
+        epi.up_packed, epi.up_scales, epi.up_biases = (_dense_view(spec, 8192 * (i + 1))
+                                                       for i, spec in enumerate(specs[4:7]))
+    name = ctypes.create_string_buffer(256)
+    status = _native.load().affon_rocm_quantized_matmul_fused_select(ctypes.byref(desc), ctypes.byref(epi), name, 256)
+    if status != _native.OK:
+        raise TypeError(f"no rocm quantized_matmul implementation: {_native.last_error()}")
+    return name.value.decode()
+
+
+# ---- formal element-wise ops (lowered into quantized_matmul epilogues) ----
+
+def _formal_pair(name: str, a: Any, b: Any) -> None:
+    if not isinstance(a, FormalTensor) or not isinstance(b, FormalTensor):
+        if isinstance(a, FormalTensor) != isinstance(b, FormalTensor):
+            raise TypeError(f"{name} cannot mix formal and evaluated tensors")
+        raise TypeError(f"{name} of evaluated tensors has no rocm kernel: author it in a Program after "
+                        "quantized_matmul, or call quantized_linear / quantized_silu_gate")
+    if a.builder is not b.builder:
+        raise TypeError(f"{name} operands must belong to the same Program")
+
+
+def _broadcast(name: str, a: TensorSpec, b: TensorSpec) -> TensorSpec:
+    """Same shape, or a rank-one operand matching the other's last axis."""
+    if a.shape == b.shape:
+        shape = a.shape
+    elif len(b.shape) == 1 and len(a.shape) >= 1 and b.shape[0] == a.shape[-1]:
+        shape = a.shape
+    elif len(a.shape) == 1 and len(b.shape) >= 1 and a.shape[0] == b.shape[-1]:
+        shape = b.shape
+    else:
+        raise TypeError(f"{name} operand shapes {a.shape} and {b.shape} do not broadcast")
+    if a.dtype == "u32" or b.dtype == "u32":
+        raise TypeError(f"{name} requires f32/bf16 tensors")
+    return TensorSpec("f32" if "f32" in (a.dtype, b.dtype) else a.dtype, shape)
+
+
+def add(a: Any, b: Any) -> FormalTensor:
+    """Formal element-wise add (src/js/ops.ts:51)."""
+    _formal_pair("add", a, b)
+    return a.builder.emit("add", (a, b), _broadcast("add", a.spec, b.spec), {})
+
+
+def mul(a: Any, b: Any) -> FormalTensor:
+    """Formal element-wise multiply (src/js/ops.ts:53)."""
+    _formal_pair("mul", a, b)
+    return a.builder.emit("mul", (a, b), _broadcast("mul", a.spec, b.spec), {})
+
+
+def silu(x: Any) -> FormalTensor:
+    """Formal silu (src/js/ops.ts:91)."""
+    if not isinstance(x, FormalTensor):
+        raise TypeError("silu of an evaluated tensor has no rocm kernel: author it in a Program after "
+                        "quantized_matmul, or call quantized_silu_gate")
+    if x.dtype == "u32":
+        raise TypeError("silu requires an f32/bf16 tensor")
+    return x.builder.emit("silu", (x,), x.spec, {})
 
 
 def quantize(weights: Tensor, *, bits: int, group_size: int, param_dtype: str = "bf16") -> tuple[Tensor, Tensor, Tensor]:

@@ -272,31 +272,44 @@ LLAMA8B_LAYER = (("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 
                  ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336), ("lm_head", 128256, 4096))
 
 
-def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int) -> dict:
+def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bool = False) -> dict:
     """The Llama-8B-shaped projections at 4-bit group 64 (bf16 x, scales and
     biases; one weight seed per projection), run back to back on one stream:
     a step is the whole sequence. Weights total 4.4 GB per set, larger than
-    the MALL, so no rotation is needed."""
+    the MALL, so no rotation is needed. With ``fused`` the gate and up
+    projections run as one SiLU-gated call (silu(gate) * up written once)."""
     import affon_amd as A
     from affon_amd import ops
     lib = ops._native.load()
-    descs, outs, impls, nbytes, flops = [], [], {}, 0, 0
-    tensors = []
+    calls, impls, nbytes, flops = [], {}, 0, 0
+    tensors, by_name = [], {}
     for i, (name, N, K) in enumerate(LLAMA8B_LAYER):
         x = session.randn((M, K), seed=1, dtype="bf16")
         w = session.randn((N, K), seed=3 + i, std=0.02, dtype="bf16")
         packed, scales, biases = A.quantize(w, bits=4, group_size=64, param_dtype="bf16")
         del w
-        out = session.empty("f32", (M, N))
-        descs.append(ops._descriptor(x, packed, scales, biases, 4, 64, out, "auto", "backend_equivalent"))
-        impls[name] = A.selected_implementation(x, packed, scales, biases, bits=4, group_size=64)
-        tensors.append((x, packed, scales, biases, out))
+        by_name[name] = (x, packed, scales, biases)
         nbytes += algorithmic_bytes(M, N, K, 4, 64, 2, 2)
         flops += 2 * M * N * K
+        if fused and name == "up":
+            gx, gp, gs, gb = by_name["gate"]
+            epi = ops._epilogue(up=(packed, scales, biases))
+            calls[-1] = (lib.affon_rocm_quantized_matmul_fused, calls[-1][1], epi)
+            impls["gate+up"] = A.fused_plan(gx, gp, gs, gb, bits=4, group_size=64, up=(packed, scales, biases))
+            del impls["gate"]
+            nbytes -= M * N * 4  # one [M, N] output instead of two
+            tensors.append((x, packed, scales, biases, epi))
+            continue
+        out = session.empty("f32", (M, N))
+        calls.append((lib.affon_rocm_quantized_matmul,
+                       ops._descriptor(x, packed, scales, biases, 4, 64, out, "auto", "backend_equivalent"), None))
+        impls[name] = A.selected_implementation(x, packed, scales, biases, bits=4, group_size=64)
+        tensors.append((x, packed, scales, biases, out))
 
     def launch_all():
-        for d in descs:
-            status = lib.affon_rocm_quantized_matmul(session._handle, ctypes.byref(d))
+        for fn, desc, epi in calls:
+            status = fn(session._handle, ctypes.byref(desc)) if epi is None else \
+                fn(session._handle, ctypes.byref(desc), ctypes.byref(epi))
             if status != 0:
                 from affon_amd import _native
                 raise RuntimeError(_native.last_error())
@@ -313,16 +326,21 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int) -> dict:
     hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
     hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
     session.synchronize()
+    # The median of several timed replays (one replay is `steps` layers): a
+    # single replay varies with the GPU's clock state by several percent.
     start, stop = hip.event(), hip.event()
-    hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-    hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-    hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
-    hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
-    ms = ctypes.c_float()
-    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+    times = []
+    for _ in range(5):
+        hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+        hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+        hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+        hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+        times.append(ms.value)
     hip.lib.hipGraphExecDestroy(exe)
     hip.lib.hipGraphDestroy(graph)
-    t = ms.value / steps
+    t = sorted(times)[len(times) // 2] / steps
     tensors.clear()
     return {"implementations": impls, "us_per_layer": round(t * 1e3, 2),
             "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -419,6 +437,9 @@ def main() -> int:
         name = f"llama8b_layer_4bit_g64_m{M}"
         if want(name):
             extras[name] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup)
+        if want(name + "_fused_gate_up"):
+            extras[name + "_fused_gate_up"] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup,
+                                                             fused=True)
     if want("decode_4bit_g64_f32_4096"):
         record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
                                                     x_dtype="f32", p_dtype="f32"))
