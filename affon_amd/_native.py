@@ -79,6 +79,10 @@ SIGNATURES = {
     "affon_rocm_quantized_matmul_fused": (c_int, [c_void_p, ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue)]),
     "affon_rocm_quantized_matmul_fused_select": (c_int, [ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue), c_char_p,
                                                          c_size_t]),
+    "affon_rocm_quantized_matmul_grouped": (c_int, [c_void_p, ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue),
+                                                    c_size_t]),
+    "affon_rocm_quantized_matmul_grouped_select": (c_int, [ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue), c_size_t,
+                                                           c_char_p, c_size_t]),
     "affon_rocm_quantized_matmul_capabilities": (c_char_p, []),
     "compute_core_run_quantized_matmul_f32": (c_int, [
         c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t,

@@ -371,13 +371,21 @@ class Executable:
         policy = self.options["numericalPolicy"]
         if step.kind == "quantized_matmul":
             return self._ops.select_for_specs(specs, step.options, policy)
+        if step.kind == "grouped":
+            members = [[self.program.nodes[i]["spec"] for i in m.operands] for m in step.members]
+            return self._ops.grouped_select_for_specs(members, step.options, policy)
         return self._ops.fused_select_for_specs(step.kind, specs, step.options, policy)
 
     def explain(self) -> dict[str, Any]:
         names = {"quantized_matmul": "quantized_matmul", "bias": "quantized_matmul+add",
                  "silu_gate": "quantized_matmul+silu+quantized_matmul+mul"}
-        physical = [{"op": names[step.kind], "implementation_id": impl, "implementation_version": 1,
-                     "options": step.options, "nodes": sorted(step.absorbed + [step.node])}
+
+        def op(step):
+            if step.kind == "grouped":
+                return "grouped(" + ",".join(names[m.kind] for m in step.members) + ")"
+            return names[step.kind]
+        physical = [{"op": op(step), "implementation_id": impl, "implementation_version": 1,
+                     "options": step.options, "nodes": step.nodes}
                     for step, impl in zip(self._steps, self._implementations)]
         return {"program": self.program.name, "device": self.session.device, "options": dict(self.options),
                 "executable": {"physical_nodes": physical}}
@@ -400,6 +408,12 @@ class Executable:
             bits, group = step.options["bits"], step.options["group_size"]
             if step.kind == "quantized_matmul":
                 values[step.node] = self._ops._run_quantized_matmul(*operands, bits, group, policy=policy)
+            elif step.kind == "grouped":
+                projections = [tuple(values[i] for i in m.operands[1:]) for m in step.members]
+                outs = self._ops.quantized_matmul_grouped(operands[0], projections, bits=bits, group_size=group,
+                                                          policy=policy)
+                for m, out in zip(step.members, outs):
+                    values[m.node] = out
             elif step.kind == "bias":
                 self._ops._check_bias(operands[4], operands[1].shape[0])
                 epi = self._ops._epilogue(output_bias=operands[4])

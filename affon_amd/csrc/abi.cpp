@@ -14,6 +14,7 @@
 #include <limits>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "affon_rocm.h"
 #include "internal.h"
@@ -480,6 +481,9 @@ int plan_fused(const affon_rocm_qmm_desc* d, const affon_rocm_qmm_epilogue* e, F
   }
 }
 
+std::string fused_text(const FusedPlan& plan);
+int copy_id(const std::string& text, char* id, size_t cap);
+
 }  // namespace
 
 extern "C" {
@@ -509,6 +513,62 @@ int affon_rocm_quantized_matmul_fused_select(const affon_rocm_qmm_desc* desc, co
   FusedPlan plan;
   int status = plan_fused(desc, epilogue, &plan);
   if (status != AFFON_ROCM_OK) return status;
+  return copy_id(fused_text(plan), id, cap);
+}
+
+}  // extern "C"
+
+namespace {
+
+bool same_view(const affon_rocm_view& a, const affon_rocm_view& b) {
+  return a.data == b.data && a.byte_offset == b.byte_offset && a.shape[0] == b.shape[0] && a.shape[1] == b.shape[1] &&
+         a.stride[0] == b.stride[0] && a.stride[1] == b.stride[1] && a.dtype == b.dtype;
+}
+
+// A grouped call: every member's plan, and whether they run as one launch.
+struct GroupPlan {
+  FusedPlan members[affon::kMaxGroup];
+  std::vector<FusedPlan> many;  // more members than one launch takes
+  size_t count = 0;
+  bool one_launch = false;
+  const FusedPlan& at(size_t i) const { return count <= affon::kMaxGroup ? members[i] : many[i]; }
+};
+
+int plan_grouped(const affon_rocm_qmm_desc* descs, const affon_rocm_qmm_epilogue* epilogues, size_t count,
+                 GroupPlan* plan) {
+  if (descs == nullptr || count == 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "grouped quantized_matmul needs at least one descriptor");
+  if (count > affon::kMaxGroup) plan->many.resize(count);
+  plan->count = count;
+  affon_rocm_qmm_epilogue none;
+  std::memset(&none, 0, sizeof(none));
+  none.kind = AFFON_ROCM_EPILOGUE_NONE;
+  for (size_t i = 0; i < count; ++i) {
+    const affon_rocm_qmm_desc& d = descs[i];
+    if (i > 0 && (!same_view(d.input, descs[0].input) || d.bits != descs[0].bits ||
+                  d.group_size != descs[0].group_size || d.implementation != descs[0].implementation ||
+                  d.numerical_policy != descs[0].numerical_policy))
+      return fail(AFFON_ROCM_INVALID_SHAPE, "grouped quantized_matmul descriptors must share the input and options");
+    const affon_rocm_qmm_epilogue* e = epilogues != nullptr ? &epilogues[i] : &none;
+    if (e->kind != AFFON_ROCM_EPILOGUE_NONE && e->kind != AFFON_ROCM_EPILOGUE_BIAS)
+      return fail(AFFON_ROCM_INVALID_SHAPE, "grouped quantized_matmul takes no epilogue or an output bias per call");
+    FusedPlan& member = count <= affon::kMaxGroup ? plan->members[i] : plan->many[i];
+    int status = plan_fused(&d, e, &member);
+    if (status != AFFON_ROCM_OK) return status;
+  }
+  if (count >= 2 && count <= affon::kMaxGroup) {
+    affon::QmmProblem problems[affon::kMaxGroup];
+    bool all_gemv = true;
+    for (size_t i = 0; i < count; ++i) {
+      problems[i] = plan->members[i].first;
+      all_gemv = all_gemv && plan->members[i].first_c->impl == AFFON_ROCM_IMPL_GEMV;
+    }
+    plan->one_launch = all_gemv && affon::gemv_group_supports(problems, static_cast<int>(count));
+  }
+  return AFFON_ROCM_OK;
+}
+
+std::string fused_text(const FusedPlan& plan) {
   std::string text = plan.first_c->id;
   switch (plan.first.epi.kind) {
     case affon::kEpiBias: text += "[bias]"; break;
@@ -516,11 +576,63 @@ int affon_rocm_quantized_matmul_fused_select(const affon_rocm_qmm_desc* desc, co
     default: break;
   }
   if (plan.two) text += std::string(";") + plan.second_c->id + "[gate_mul]";
+  return text;
+}
+
+int copy_id(const std::string& text, char* id, size_t cap) {
   if (id != nullptr && cap > 0) {
     std::strncpy(id, text.c_str(), cap - 1);
     id[cap - 1] = '\0';
   }
   return AFFON_ROCM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int affon_rocm_quantized_matmul_grouped(affon_rocm_session* session, const affon_rocm_qmm_desc* descs,
+                                        const affon_rocm_qmm_epilogue* epilogues, size_t count) {
+  clear_error();
+  GroupPlan plan;
+  int status = plan_grouped(descs, epilogues, count, &plan);
+  if (status != AFFON_ROCM_OK) return status;
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  affon::Launch launch;
+  launch.stream = session->stream;
+  launch.workspace = session->workspace;
+  if (plan.one_launch) {
+    affon::QmmProblem problems[affon::kMaxGroup];
+    for (size_t i = 0; i < count; ++i) problems[i] = plan.members[i].first;
+    hipError_t e = affon::gemv_group_launch(problems, static_cast<int>(count), launch);
+    if (e != hipSuccess) return hip_fail(e, "rocm_quantized_matmul.gemv (grouped)");
+    return AFFON_ROCM_OK;
+  }
+  for (size_t i = 0; i < count; ++i) {
+    const FusedPlan& member = plan.at(i);
+    hipError_t e = member.first_c->launch(member.first, launch);
+    if (e != hipSuccess) return hip_fail(e, member.first_c->id);
+  }
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_quantized_matmul_grouped_select(const affon_rocm_qmm_desc* descs,
+                                               const affon_rocm_qmm_epilogue* epilogues, size_t count, char* id,
+                                               size_t cap) {
+  clear_error();
+  GroupPlan plan;
+  int status = plan_grouped(descs, epilogues, count, &plan);
+  if (status != AFFON_ROCM_OK) return status;
+  if (plan.one_launch) {
+    bool bias = false;
+    for (size_t i = 0; i < count; ++i) bias = bias || plan.members[i].first.epi.kind == affon::kEpiBias;
+    return copy_id(std::string(plan.members[0].first_c->id) + "[grouped:" + std::to_string(count) +
+                       (bias ? ",bias]" : "]"),
+                   id, cap);
+  }
+  std::string text;
+  for (size_t i = 0; i < count; ++i) text += (i ? ";" : "") + fused_text(plan.at(i));
+  return copy_id(text, id, cap);
 }
 
 const char* affon_rocm_quantized_matmul_capabilities(void) {

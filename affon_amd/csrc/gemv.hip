@@ -286,6 +286,32 @@ bool gemv_pair_supports(const QmmProblem& p) {
          reinterpret_cast<uintptr_t>(p.epi.s2) % pbytes == 0 && reinterpret_cast<uintptr_t>(p.epi.b2) % pbytes == 0;
 }
 
+bool gemv_group_supports(const QmmProblem* group, int count) {
+  if (count < 1 || count > kMaxGroup || count > gemv1::kMaxSegments) return false;
+  const QmmProblem& p = group[0];
+  for (int i = 0; i < count; ++i) {
+    const QmmProblem& q = group[i];
+    if (!gemv1_supports(q) || q.epi.kind == kEpiSiluPair || q.epi.kind == kEpiGateMul) return false;
+    if (q.x != p.x || q.K != p.K || q.bits != p.bits || q.group != p.group || q.x_dtype != p.x_dtype ||
+        q.p_dtype != p.p_dtype || q.ws0 != p.ws0 || q.ss0 != p.ss0 || q.bs0 != p.bs0)
+      return false;
+    if (q.epi.kind == kEpiBias) {
+      for (int j = 0; j < count; ++j)
+        if (group[j].epi.kind == kEpiBias && group[j].epi.bias_bf16 != q.epi.bias_bf16) return false;
+    }
+  }
+  return true;
+}
+
+hipError_t gemv_group_launch(const QmmProblem* group, int count, const Launch& l) {
+  if (!gemv_group_supports(group, count)) return hipErrorInvalidValue;
+  switch (group[0].bits) {
+    case 2: return gemv1_group_launch_b2(group, count, l.stream);
+    case 4: return gemv1_group_launch_b4(group, count, l.stream);
+    default: return gemv1_group_launch_b8(group, count, l.stream);
+  }
+}
+
 hipError_t gemv_launch(const QmmProblem& p, const Launch& l) {
   hipStream_t stream = l.stream;
   if (p.epi.kind == kEpiSiluPair && !gemv_pair_supports(p)) return hipErrorInvalidValue;

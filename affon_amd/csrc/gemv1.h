@@ -20,10 +20,15 @@
 //     parameters are applied once per chunk: y += s * sum(x*q) + b * sum(x);
 //   * rows are reduced across the wave with butterfly shuffles and across the
 //     K-parts of a workgroup through LDS;
-//   * with PAIR, the wave's first R/2 rows are rows of a gate projection and
-//     the last R/2 the same rows of an up projection (same activations, same
-//     strides), and the wave stores silu(gate) * up: the SiLU-gated
-//     feed-forward input in one pass over both weight matrices.
+//   * in paired mode the wave's first R/2 rows are rows of a gate projection
+//     and the last R/2 the same rows of an up projection (same activations,
+//     same strides), and the wave stores silu(gate) * up: the SiLU-gated
+//     feed-forward input in one pass over both weight matrices;
+//   * in grouped mode one launch runs up to kMaxSegments projections that
+//     share the activation row (a decoder block's query, key and value): the
+//     launch's rows are the projections' rows one after another, each
+//     projection starting on a multiple of 8, so every wave lies in one
+//     projection and picks its pointers once.
 #pragma once
 
 #include "device.h"
@@ -37,6 +42,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+constexpr int kMaxSegments = 4;
+
+// Kernel modes.
+constexpr int kPlain = 0, kPaired = 1, kGrouped = 2;
 
 struct Args {
   const uint32_t* w;
@@ -53,7 +62,27 @@ struct Args {
   int part;    // chunks per K-part
   int ks;      // K-parts per row (waves per row block)
   Epilogue epi;
+  // Grouped mode: projection i owns launch rows [first[i], first[i] + n[i])
+  // (first[0] = 0, each first a multiple of 8), with the strides above.
+  int segments;
+  int64_t seg_first[kMaxSegments];
+  int64_t seg_n[kMaxSegments];
+  const uint32_t* seg_w[kMaxSegments];
+  const uint8_t* seg_s[kMaxSegments];
+  const uint8_t* seg_b[kMaxSegments];
+  float* seg_out[kMaxSegments];
+  const uint8_t* seg_bias[kMaxSegments];  // output bias (element type epi.bias_bf16) or null
 };
+
+// a[seg] for a uniform seg < kMaxSegments, by selects (no dynamic indexing of
+// the kernel argument block).
+template <typename T>
+__device__ __forceinline__ T pick(const T (&a)[kMaxSegments], int seg) {
+  T v = a[0];
+#pragma unroll
+  for (int j = 1; j < kMaxSegments; ++j) v = seg == j ? a[j] : v;
+  return v;
+}
 
 template <int BITS>
 constexpr int chunk_values() { return 128 / BITS; }
@@ -326,8 +355,9 @@ __device__ __forceinline__ void stage_pieces(u32x4_t v, int p, int count, uint4*
   }
 }
 
-template <int BITS, typename XT, typename PT, int R, int CPL, bool PAIR>
+template <int BITS, typename XT, typename PT, int R, int CPL, int MODE>
 __global__ __launch_bounds__(kThreads) void kernel(Args a) {
+  constexpr bool PAIR = MODE == kPaired;
   static_assert(!PAIR || R % 2 == 0, "paired rows");
   constexpr int RO = PAIR ? R / 2 : R;  // output rows per wave
   using XS = XStage<BITS, XT>;
@@ -343,14 +373,35 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int kp = wave % a.ks;
-  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * RO;
+  int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * RO;
   const int c_begin = kp * a.part;
   const int c_end = min(a.chunks, c_begin + a.part);
+  // The wave's projection: the launch's, or in grouped mode the one whose
+  // rows hold n0 (all uniform).
+  const uint32_t* W = a.w;
+  const uint8_t* S = a.s;
+  const uint8_t* B = a.b;
+  float* out = a.out;
+  int64_t N = a.N;
+  Epilogue epi = a.epi;
+  if constexpr (MODE == kGrouped) {
+    int seg = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxSegments; ++j) seg = j < a.segments && n0 >= a.seg_first[j] ? j : seg;
+    n0 -= pick(a.seg_first, seg);
+    N = pick(a.seg_n, seg);
+    W = pick(a.seg_w, seg);
+    S = pick(a.seg_s, seg);
+    B = pick(a.seg_b, seg);
+    out = pick(a.seg_out, seg);
+    epi.bias = pick(a.seg_bias, seg);
+    epi.kind = epi.bias != nullptr ? kEpiBias : kEpiNone;
+  }
   // Row r of the wave: output row n0 + r % RO of the first (r < RO) or the
   // second projection.
   auto row_of = [&](int r) {
     const int64_t n = n0 + (r % RO);
-    return n < a.N ? n : a.N - 1;
+    return n < N ? n : N - 1;
   };
   auto second = [](int r) { return PAIR && r >= RO; };
 
@@ -378,8 +429,8 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t n = row_of(r);
-      const uint8_t* srow = (second(r) ? a.epi.s2 : a.s) + n * a.ss0 * PT::bytes;
-      const uint8_t* brow = (second(r) ? a.epi.b2 : a.b) + n * a.bs0 * PT::bytes;
+      const uint8_t* srow = (second(r) ? a.epi.s2 : S) + n * a.ss0 * PT::bytes;
+      const uint8_t* brow = (second(r) ? a.epi.b2 : B) + n * a.bs0 * PT::bytes;
       if constexpr (PT::bytes == 2) {
         sraw[r][i] = *reinterpret_cast<const uint16_t*>(srow + goff);
         braw[r][i] = *reinterpret_cast<const uint16_t*>(brow + goff);
@@ -395,7 +446,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t n = row_of(r);
-    const u32x4_t* row = reinterpret_cast<const u32x4_t*>((second(r) ? a.epi.w2 : a.w) + n * a.ws0);
+    const u32x4_t* row = reinterpret_cast<const u32x4_t*>((second(r) ? a.epi.w2 : W) + n * a.ws0);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = c_begin + lane + 64 * i;
@@ -464,11 +515,11 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
   // Lane o < RO stores output row n0 + o.
   auto finish = [&](float v, float up) {
-    if (n0 + lane >= a.N) return;
+    if (n0 + lane >= N) return;
     if constexpr (PAIR)
-      a.out[n0 + lane] = silu(v) * up;
+      out[n0 + lane] = silu(v) * up;
     else
-      store_output(a.epi, a.out, n0 + lane, n0 + lane, v);
+      store_output(epi, out, n0 + lane, n0 + lane, v);
   };
   if (a.ks == 1) {
     if (lane < RO) {
@@ -497,14 +548,14 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
 }
 
-template <int BITS, typename XT, typename PT, int R, int CPL, bool PAIR>
+template <int BITS, typename XT, typename PT, int R, int CPL, int MODE>
 hipError_t launch(const Args& a, hipStream_t stream) {
-  constexpr int RO = PAIR ? R / 2 : R;
+  constexpr int RO = MODE == kPaired ? R / 2 : R;
   const size_t lds = lds_size<BITS, XT, R>(a.chunks);
   const int64_t row_blocks = (a.N + RO - 1) / RO;
   const int64_t per_block = kWaves / a.ks;
   const unsigned blocks = static_cast<unsigned>((row_blocks + per_block - 1) / per_block);
-  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL, PAIR>), dim3(blocks), dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL, MODE>), dim3(blocks), dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
 
@@ -515,5 +566,8 @@ bool gemv1_supports(const QmmProblem& p);
 hipError_t gemv1_launch_b2(const QmmProblem& p, hipStream_t stream);
 hipError_t gemv1_launch_b4(const QmmProblem& p, hipStream_t stream);
 hipError_t gemv1_launch_b8(const QmmProblem& p, hipStream_t stream);
+hipError_t gemv1_group_launch_b2(const QmmProblem* group, int count, hipStream_t stream);
+hipError_t gemv1_group_launch_b4(const QmmProblem* group, int count, hipStream_t stream);
+hipError_t gemv1_group_launch_b8(const QmmProblem* group, int count, hipStream_t stream);
 
 }  // namespace affon

@@ -5,5 +5,8 @@
 namespace affon {
 
 hipError_t gemv1_launch_b4(const QmmProblem& p, hipStream_t stream) { return gemv1::dispatch_bits<4>(p, stream); }
+hipError_t gemv1_group_launch_b4(const QmmProblem* group, int count, hipStream_t stream) {
+  return gemv1::dispatch_group_bits<4>(group, count, stream);
+}
 
 }  // namespace affon

@@ -9,7 +9,8 @@
 // 14336x4096 and 4096x14336, 4-bit 14336x4096, 4096x14336, 4096x4096,
 // 1024x4096 and 128256x4096 (bf16), and 4-bit 4096x4096 with f32 operands.
 // Paired gate/up problems choose among the even-R variants the same way,
-// counting R/2 output rows per wave.
+// counting R/2 output rows per wave; grouped launches count the rows of all
+// their projections (each padded to a multiple of 8).
 #pragma once
 
 #include <map>
@@ -38,26 +39,24 @@ size_t lds_bytes(int chunks) {
   return lds_size<BITS, XT, R>(chunks);
 }
 
-#define AFFON_GEMV1_VARIANT(R, CPL, PAIR)                                            \
-  {R, CPL, launch<BITS, XT, PT, R, CPL, PAIR>,                                        \
-   reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL, PAIR>), lds_bytes<BITS, XT, R>}
+#define AFFON_GEMV1_VARIANT(R, CPL)                                                     \
+  {R, CPL, launch<BITS, XT, PT, R, CPL, MODE>,                                           \
+   reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL, MODE>), lds_bytes<BITS, XT, R>}
 
-template <int BITS, typename XT, typename PT, bool PAIR>
+template <int BITS, typename XT, typename PT, int MODE>
 const Variant* variants(int* count) {
-  if constexpr (PAIR) {
+  if constexpr (MODE == kPaired) {
     static const Variant table[] = {
-        AFFON_GEMV1_VARIANT(2, 1, true), AFFON_GEMV1_VARIANT(4, 1, true), AFFON_GEMV1_VARIANT(8, 1, true),
-        AFFON_GEMV1_VARIANT(2, 2, true), AFFON_GEMV1_VARIANT(4, 2, true), AFFON_GEMV1_VARIANT(2, 4, true),
-        AFFON_GEMV1_VARIANT(4, 4, true),
+        AFFON_GEMV1_VARIANT(2, 1), AFFON_GEMV1_VARIANT(4, 1), AFFON_GEMV1_VARIANT(8, 1), AFFON_GEMV1_VARIANT(2, 2),
+        AFFON_GEMV1_VARIANT(4, 2), AFFON_GEMV1_VARIANT(2, 4), AFFON_GEMV1_VARIANT(4, 4),
     };
     *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
     return table;
   } else {
     static const Variant table[] = {
-        AFFON_GEMV1_VARIANT(1, 1, false), AFFON_GEMV1_VARIANT(2, 1, false), AFFON_GEMV1_VARIANT(4, 1, false),
-        AFFON_GEMV1_VARIANT(8, 1, false), AFFON_GEMV1_VARIANT(1, 2, false), AFFON_GEMV1_VARIANT(2, 2, false),
-        AFFON_GEMV1_VARIANT(4, 2, false), AFFON_GEMV1_VARIANT(1, 4, false), AFFON_GEMV1_VARIANT(2, 4, false),
-        AFFON_GEMV1_VARIANT(4, 4, false),
+        AFFON_GEMV1_VARIANT(1, 1), AFFON_GEMV1_VARIANT(2, 1), AFFON_GEMV1_VARIANT(4, 1), AFFON_GEMV1_VARIANT(8, 1),
+        AFFON_GEMV1_VARIANT(1, 2), AFFON_GEMV1_VARIANT(2, 2), AFFON_GEMV1_VARIANT(4, 2), AFFON_GEMV1_VARIANT(1, 4),
+        AFFON_GEMV1_VARIANT(2, 4), AFFON_GEMV1_VARIANT(4, 4),
     };
     *count = static_cast<int>(sizeof(table) / sizeof(table[0]));
     return table;
@@ -94,8 +93,11 @@ inline int blocks_per_cu(const void* fn, size_t lds) {
   return blocks;
 }
 
-template <int BITS, typename XT, typename PT, bool PAIR>
-hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
+// p: the problem (grouped mode: the first projection; group holds all
+// `count` projections, which share everything but the weights and outputs).
+template <int BITS, typename XT, typename PT, int MODE>
+hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hipStream_t stream) {
+  constexpr bool PAIR = MODE == kPaired;
   Args a;
   a.w = p.w;
   a.ws0 = p.ws0;
@@ -107,16 +109,43 @@ hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
   a.out = p.out;
   a.epi = p.epi;
   a.N = p.N;
+  a.segments = 1;
+  for (int i = 0; i < kMaxSegments; ++i) {
+    a.seg_first[i] = 0;
+    a.seg_n[i] = 0;
+    a.seg_w[i] = nullptr;
+    a.seg_s[i] = a.seg_b[i] = a.seg_bias[i] = nullptr;
+    a.seg_out[i] = nullptr;
+  }
+  if constexpr (MODE == kGrouped) {
+    if (count < 1 || count > kMaxSegments) return hipErrorInvalidValue;
+    int64_t first = 0;
+    for (int i = 0; i < count; ++i) {
+      a.seg_first[i] = first;
+      a.seg_n[i] = group[i].N;
+      a.seg_w[i] = group[i].w;
+      a.seg_s[i] = group[i].s;
+      a.seg_b[i] = group[i].b;
+      a.seg_out[i] = group[i].out;
+      a.seg_bias[i] = group[i].epi.kind == kEpiBias ? group[i].epi.bias : nullptr;
+      first += (group[i].N + 7) / 8 * 8;
+    }
+    a.segments = count;
+    a.N = a.seg_first[count - 1] + a.seg_n[count - 1];
+    a.epi.bias_bf16 = 0;
+    for (int i = 0; i < count; ++i)
+      if (group[i].epi.kind == kEpiBias) a.epi.bias_bf16 = group[i].epi.bias_bf16;
+  }
   a.chunks = static_cast<int>(p.K * BITS / 128);
   a.cpg_shift = 0;
   while ((int64_t(1) << a.cpg_shift) * chunk_values<BITS>() < p.group) ++a.cpg_shift;
-  int count = 0;
-  const Variant* table = variants<BITS, XT, PT, PAIR>(&count);
+  int nvariants = 0;
+  const Variant* table = variants<BITS, XT, PT, MODE>(&nvariants);
   const int cus = device_cus();
   const Variant* best = nullptr;
   int best_ks = 0;
   int64_t best_rounds = 0, best_waves = 0;
-  for (int i = 0; i < count; ++i) {
+  for (int i = 0; i < nvariants; ++i) {
     const Variant& v = table[i];
     int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
     if (ks == 3) ks = 4;
@@ -127,7 +156,7 @@ hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
     if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
     const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
     const int rows_out = PAIR ? v.R / 2 : v.R;
-    const int64_t waves = (p.N + rows_out - 1) / rows_out * ks;
+    const int64_t waves = (a.N + rows_out - 1) / rows_out * ks;
     const int64_t rounds = (waves + capacity - 1) / capacity;
     const bool better = best == nullptr || rounds < best_rounds ||
                         (rounds == best_rounds && (ks < best_ks || (ks == best_ks && waves > best_waves)));
@@ -144,20 +173,25 @@ hipError_t dispatch(const QmmProblem& p, hipStream_t stream) {
   return best->launch(a, stream);
 }
 
-template <int BITS, bool PAIR>
-hipError_t dispatch_pair(const QmmProblem& p, hipStream_t stream) {
+template <int BITS, int MODE>
+hipError_t dispatch_mode(const QmmProblem& p, const QmmProblem* group, int count, hipStream_t stream) {
   if (p.x_dtype == AFFON_ROCM_BF16) {
-    if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, BF16, BF16, PAIR>(p, stream);
-    return dispatch<BITS, BF16, F32, PAIR>(p, stream);
+    if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, BF16, BF16, MODE>(p, group, count, stream);
+    return dispatch<BITS, BF16, F32, MODE>(p, group, count, stream);
   }
-  if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, F32, BF16, PAIR>(p, stream);
-  return dispatch<BITS, F32, F32, PAIR>(p, stream);
+  if (p.p_dtype == AFFON_ROCM_BF16) return dispatch<BITS, F32, BF16, MODE>(p, group, count, stream);
+  return dispatch<BITS, F32, F32, MODE>(p, group, count, stream);
 }
 
 template <int BITS>
 hipError_t dispatch_bits(const QmmProblem& p, hipStream_t stream) {
-  if (p.epi.kind == kEpiSiluPair) return dispatch_pair<BITS, true>(p, stream);
-  return dispatch_pair<BITS, false>(p, stream);
+  if (p.epi.kind == kEpiSiluPair) return dispatch_mode<BITS, kPaired>(p, nullptr, 0, stream);
+  return dispatch_mode<BITS, kPlain>(p, nullptr, 0, stream);
+}
+
+template <int BITS>
+hipError_t dispatch_group_bits(const QmmProblem* group, int count, hipStream_t stream) {
+  return dispatch_mode<BITS, kGrouped>(group[0], group, count, stream);
 }
 
 }  // namespace gemv1

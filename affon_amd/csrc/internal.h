@@ -64,6 +64,12 @@ bool gemv_supports(const QmmProblem& p);
 // in one launch.
 bool gemv_pair_supports(const QmmProblem& p);
 hipError_t gemv_launch(const QmmProblem& p, const Launch& l);
+// Grouped launch of up to 4 M = 1 problems that share the activation row,
+// bits, group size, dtypes and strides (each with no epilogue or an output
+// bias of one element type).
+constexpr int kMaxGroup = 4;
+bool gemv_group_supports(const QmmProblem* group, int count);
+hipError_t gemv_group_launch(const QmmProblem* group, int count, const Launch& l);
 
 bool gemv_mfma_supports(const QmmProblem& p);
 hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l);

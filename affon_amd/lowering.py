@@ -13,6 +13,10 @@ are absorbed into the projection kernel's output epilogue:
   operand order), with both projections reading the same input with the same
   options and weight specs, becomes one ``silu_gate`` step.
 
+Plain and bias steps that read the same input with the same options (a
+block's query, key and value) are then gathered, up to four at a time, into
+one ``grouped`` step: one launch where the M = 1 kernel takes them all.
+
 An absorbed node must have exactly one user and must not be a Program output.
 Any element-wise node that does not fit a pattern has no rocm kernel and is
 rejected at compile time, as the reference compiler rejects an operation its
@@ -28,15 +32,27 @@ ELEMENTWISE = ("add", "mul", "silu")
 
 @dataclass
 class Step:
-    """One launch sequence: ``kind`` is "quantized_matmul", "bias" or
-    "silu_gate"; ``node`` the node whose value it produces; ``operands`` the
-    node ids it reads (x, packed, scales, biases, then the bias or the up
-    projection's packed, scales, biases); ``absorbed`` the node ids folded in."""
+    """One launch sequence: ``kind`` is "quantized_matmul", "bias",
+    "silu_gate" or "grouped"; ``node`` the node whose value it produces;
+    ``operands`` the node ids it reads (x, packed, scales, biases, then the
+    bias or the up projection's packed, scales, biases); ``absorbed`` the node
+    ids folded in; a grouped step's ``members`` are plain and bias steps."""
     kind: str
     node: int
     operands: list[int]
     options: dict[str, Any]
     absorbed: list[int] = field(default_factory=list)
+    members: list["Step"] = field(default_factory=list)
+
+    @property
+    def nodes(self) -> list[int]:
+        """Every node the step computes or absorbs."""
+        if self.members:
+            return sorted(n for m in self.members for n in m.nodes)
+        return sorted(self.absorbed + [self.node])
+
+
+MAX_GROUP = 4
 
 
 def _users(nodes: Sequence[dict[str, Any]]) -> dict[int, list[int]]:
@@ -115,4 +131,32 @@ def lower(nodes: Sequence[dict[str, Any]], outputs: Sequence[int]) -> list[Step]
         if n["id"] in pending:
             ordered.append(pending[n["id"]])
         ordered.extend(s for s in steps if s.node == n["id"])
-    return ordered
+    return _group(ordered, by_id)
+
+
+def _group(steps: list[Step], by_id: dict[int, dict[str, Any]]) -> list[Step]:
+    """Gathers plain and bias steps with the same input and options into
+    grouped steps, placed where the first member was. Members' other operands
+    must be Program arguments, so no step in between can produce them."""
+    def groupable(s: Step) -> bool:
+        return s.kind in ("quantized_matmul", "bias") and all(by_id[o]["kind"] == "argument" for o in s.operands[1:])
+
+    result: list[Step] = []
+    taken: set[int] = set()
+    for i, s in enumerate(steps):
+        if i in taken:
+            continue
+        members = [s]
+        if groupable(s):
+            for j in range(i + 1, len(steps)):
+                t = steps[j]
+                if len(members) == MAX_GROUP:
+                    break
+                if j not in taken and groupable(t) and t.operands[0] == s.operands[0] and t.options == s.options:
+                    members.append(t)
+                    taken.add(j)
+        if len(members) == 1:
+            result.append(s)
+        else:
+            result.append(Step("grouped", s.node, [s.operands[0]], s.options, members=members))
+    return result

@@ -228,6 +228,58 @@ def fused_plan(input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, *,
     return name.value.decode()
 
 
+def _projection_parts(projection: Any) -> tuple[tuple[Tensor, Tensor, Tensor], Tensor | None]:
+    if not isinstance(projection, (tuple, list)) or len(projection) not in (3, 4) or \
+            not all(isinstance(t, Tensor) for t in projection):
+        raise TypeError("a grouped projection is (packed, scales, biases) or (packed, scales, biases, output_bias)")
+    return tuple(projection[:3]), (projection[3] if len(projection) == 4 else None)  # type: ignore[return-value]
+
+
+def _grouped_arrays(input: Tensor, projections: Sequence[Any], bits: int, group: int, outs: Sequence[Tensor] | None,
+                    implementation: str, policy: str):
+    if not projections:
+        raise TypeError("quantized_matmul_grouped needs at least one projection")
+    descs = (_native.QmmDesc * len(projections))()
+    epis = (_native.Epilogue * len(projections))()
+    for i, projection in enumerate(projections):
+        (w, s, b), bias = _projection_parts(projection)
+        if any(t.session is not input.session for t in (w, s, b)):
+            raise TypeError("quantized_matmul_grouped operands must belong to the same Session")
+        _validate([input.spec, w.spec, s.spec, b.spec], {"bits": bits, "group_size": group})
+        if bias is not None:
+            _check_bias(bias, w.shape[0])
+        descs[i] = _descriptor(input, w, s, b, bits, group, outs[i] if outs is not None else None, implementation,
+                               policy)
+        if outs is None:
+            descs[i].output = 1
+            descs[i].output_bytes = input.shape[0] * w.shape[0] * 4
+        epis[i] = _epilogue(output_bias=bias)
+    return descs, epis
+
+
+def quantized_matmul_grouped(input: Tensor, projections: Sequence[Any], *, bits: int, group_size: int,
+                             implementation: str = "auto", policy: str = "backend_equivalent") -> list[Tensor]:
+    """Several projections of one input (a decoder block's query, key and
+    value), each ``quantized_matmul(input, packed, scales, biases)`` plus an
+    optional output bias; one launch where the M = 1 kernel takes them all."""
+    if not isinstance(input, Tensor):
+        raise TypeError("quantized_matmul_grouped requires evaluated tensors")
+    outs = [input.session.empty("f32", (input.shape[0], _projection_parts(p)[0][0].shape[0])) for p in projections]
+    descs, epis = _grouped_arrays(input, projections, bits, group_size, outs, implementation, policy)
+    _native.check(_native.load().affon_rocm_quantized_matmul_grouped(input.session._handle, descs, epis,
+                                                                      len(projections)), "Program execution failed")
+    return outs
+
+
+def grouped_plan(input: Tensor, projections: Sequence[Any], *, bits: int, group_size: int,
+                 implementation: str = "auto", policy: str = "backend_equivalent") -> str:
+    descs, epis = _grouped_arrays(input, projections, bits, group_size, None, implementation, policy)
+    name = ctypes.create_string_buffer(512)
+    _native.check(_native.load().affon_rocm_quantized_matmul_grouped_select(descs, epis, len(projections), name, 512),
+                  "select")
+    return name.value.decode()
+
+
 def selected_implementation(input: Tensor, packed: Tensor, scales: Tensor, biases: Tensor, *, bits: int,
                             group_size: int, implementation: str = "auto",
                             policy: str = "backend_equivalent") -> str:
@@ -296,6 +348,37 @@ def fused_select_for_specs(kind: str, specs: Sequence[TensorSpec], options: Mapp
                                                        for i, spec in enumerate(specs[4:7]))
     name = ctypes.create_string_buffer(256)
     status = _native.load().affon_rocm_quantized_matmul_fused_select(ctypes.byref(desc), ctypes.byref(epi), name, 256)
+    if status != _native.OK:
+        raise TypeError(f"no rocm quantized_matmul implementation: {_native.last_error()}")
+    return name.value.decode()
+
+
+def grouped_select_for_specs(members: Sequence[Sequence[TensorSpec]], options: Mapping[str, Any], policy: str) -> str:
+    """Compile-time plan of a grouped step: each member is (x, packed,
+    scales, biases[, bias]) specs sharing x."""
+    count = len(members)
+    descs = (_native.QmmDesc * count)()
+    epis = (_native.Epilogue * count)()
+    x_view = _dense_view(members[0][0], 256)
+    for i, specs in enumerate(members):
+        _validate(specs[:4], options)
+        d = descs[i]
+        d.input = x_view
+        d.packed, d.scales, d.biases = (_dense_view(spec, (1 << 20) * (4 * i + j + 1)) for j, spec in enumerate(specs[1:4]))
+        d.output = (1 << 30) + (1 << 24) * i
+        d.output_bytes = specs[0].shape[0] * specs[1].shape[0] * 4
+        d.bits = options["bits"]
+        d.group_size = options["group_size"]
+        d.implementation = _native.IMPL_AUTO
+        d.numerical_policy = policy_code(policy)
+        epis[i].kind = _native.EPILOGUE_NONE
+        if len(specs) == 5:
+            epis[i].kind = _native.EPILOGUE_BIAS
+            epis[i].bias = (1 << 31) + (1 << 20) * i
+            epis[i].bias_dtype = _native.BF16 if specs[4].dtype == "bf16" else _native.F32
+            epis[i].bias_bytes = specs[4].shape[0] * (2 if specs[4].dtype == "bf16" else 4)
+    name = ctypes.create_string_buffer(512)
+    status = _native.load().affon_rocm_quantized_matmul_grouped_select(descs, epis, count, name, 512)
     if status != _native.OK:
         raise TypeError(f"no rocm quantized_matmul implementation: {_native.last_error()}")
     return name.value.decode()

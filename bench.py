@@ -276,8 +276,9 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
     """The Llama-8B-shaped projections at 4-bit group 64 (bf16 x, scales and
     biases; one weight seed per projection), run back to back on one stream:
     a step is the whole sequence. Weights total 4.4 GB per set, larger than
-    the MALL, so no rotation is needed. With ``fused`` the gate and up
-    projections run as one SiLU-gated call (silu(gate) * up written once)."""
+    the MALL, so no rotation is needed. With ``fused`` the query, key and
+    value projections run as one grouped call and the gate and up projections
+    as one SiLU-gated call (silu(gate) * up written once)."""
     import affon_amd as A
     from affon_amd import ops
     lib = ops._native.load()
@@ -291,6 +292,19 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
         by_name[name] = (x, packed, scales, biases)
         nbytes += algorithmic_bytes(M, N, K, 4, 64, 2, 2)
         flops += 2 * M * N * K
+        if fused and name in ("k", "v"):
+            # Grouped with q: rebuild the grouped call with every member so far.
+            members = [n for n in ("q", "k", "v") if n in by_name]
+            qx = by_name["q"][0]
+            projections = [by_name[n][1:] for n in members]
+            outs = [session.empty("f32", (M, by_name[n][1].shape[0])) for n in members]
+            descs, epis = ops._grouped_arrays(qx, projections, 4, 64, outs, "auto", "backend_equivalent")
+            calls[0] = (lib.affon_rocm_quantized_matmul_grouped, descs, (epis, len(members)))
+            impls.pop("q", None)
+            impls.pop("q+k", None)
+            impls["+".join(members)] = A.grouped_plan(qx, projections, bits=4, group_size=64)
+            tensors.append((x, packed, scales, biases, outs, descs, epis))
+            continue
         if fused and name == "up":
             gx, gp, gs, gb = by_name["gate"]
             epi = ops._epilogue(up=(packed, scales, biases))
@@ -308,8 +322,12 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
 
     def launch_all():
         for fn, desc, epi in calls:
-            status = fn(session._handle, ctypes.byref(desc)) if epi is None else \
-                fn(session._handle, ctypes.byref(desc), ctypes.byref(epi))
+            if epi is None:
+                status = fn(session._handle, ctypes.byref(desc))
+            elif isinstance(epi, tuple):  # grouped: arrays of descriptors and epilogues
+                status = fn(session._handle, desc, epi[0], epi[1])
+            else:
+                status = fn(session._handle, ctypes.byref(desc), ctypes.byref(epi))
             if status != 0:
                 from affon_amd import _native
                 raise RuntimeError(_native.last_error())
@@ -437,9 +455,8 @@ def main() -> int:
         name = f"llama8b_layer_4bit_g64_m{M}"
         if want(name):
             extras[name] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup)
-        if want(name + "_fused_gate_up"):
-            extras[name + "_fused_gate_up"] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup,
-                                                             fused=True)
+        if want(name + "_fused"):
+            extras[name + "_fused"] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup, fused=True)
     if want("decode_4bit_g64_f32_4096"):
         record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
                                                     x_dtype="f32", p_dtype="f32"))

@@ -172,6 +172,24 @@ int affon_rocm_quantized_matmul_fused(affon_rocm_session* session, const affon_r
 int affon_rocm_quantized_matmul_fused_select(const affon_rocm_qmm_desc* desc, const affon_rocm_qmm_epilogue* epilogue,
                                              char* id, size_t cap);
 
+/* Several quantized_matmul calls that read the same input (a decoder block's
+ * query, key and value projections) as one call (no reference counterpart:
+ * the reference runs one matmul per projection,
+ * packages/@affon/models/src/llama/model.ts:73-75). descs[i] may differ only
+ * in packed, scales, biases and output; input, bits, group_size,
+ * implementation and numerical_policy are shared. epilogues is null or holds
+ * count entries, each AFFON_ROCM_EPILOGUE_NONE or _BIAS. Results equal count
+ * separate calls. When the M = 1 gemv kernel is selected for every call and
+ * count <= 4 (with equal strides) they run as one launch. */
+int affon_rocm_quantized_matmul_grouped(affon_rocm_session* session, const affon_rocm_qmm_desc* descs,
+                                        const affon_rocm_qmm_epilogue* epilogues, size_t count);
+
+/* Plan of a grouped call: "<id>[grouped:<count>]" (",bias]" when any call
+ * adds an output bias) for one launch, else each call's plan separated by ';'. */
+int affon_rocm_quantized_matmul_grouped_select(const affon_rocm_qmm_desc* descs,
+                                               const affon_rocm_qmm_epilogue* epilogues, size_t count, char* id,
+                                               size_t cap);
+
 /* JSON array describing every registered candidate: id, version, numerical
  * class and guard (capability registration for the rocm backend). */
 const char* affon_rocm_quantized_matmul_capabilities(void);

@@ -78,8 +78,12 @@ def test_decoder_block_programs_against_oracle(session, tmp_path, M):
     else:
         assert explained[0]["implementation_id"].endswith("[gate_mul]")
     attention_nodes = session.compile(block.attention_program(M, "bf16")).explain()["executable"]["physical_nodes"]
-    assert [n["op"] for n in attention_nodes] == ["quantized_matmul+add"] * 3
-    assert all(n["implementation_id"].endswith("[bias]") for n in attention_nodes)
+    assert [n["op"] for n in attention_nodes] == ["grouped(" + ",".join(["quantized_matmul+add"] * 3) + ")"]
+    impl = attention_nodes[0]["implementation_id"]
+    if M == 1:
+        assert impl == "rocm_quantized_matmul.gemv[grouped:3,bias]", impl
+    else:
+        assert impl.count(";") == 2 and impl.endswith("[bias]"), impl
 
 
 def test_decoder_block_rejects_mismatched_layers(session, tmp_path):

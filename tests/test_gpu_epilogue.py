@@ -1,6 +1,7 @@
-"""GPU parity of the fused output epilogues: the output-bias add and the
+"""GPU parity of the fused output epilogues (the output-bias add and the
 SiLU-gated product of two projections, applied by the kernel that stores the
-output, against the same kernels' plain outputs and the CPU oracle.
+output) and of grouped projections of one input, against the same kernels'
+plain outputs and the CPU oracle.
 
 Tolerances (stated per test): the bias epilogue must be bit-identical to the
 plain kernel's output followed by one f32 add; the two-launch SiLU gate must be
@@ -199,3 +200,57 @@ def test_epilogue_validation_leaves_output_untouched(session):
     assert lib.affon_rocm_quantized_matmul_fused(session._handle, ctypes.byref(desc), None) == _native.INVALID_SHAPE
     session.synchronize()
     np.testing.assert_array_equal(out.numpy(), np.full((1, 64), 7.0, np.float32))
+
+
+@pytest.mark.parametrize("x_dtype,p_dtype,bits", [("bf16", "bf16", 4), ("f32", "f32", 8), ("bf16", "f32", 2)])
+@pytest.mark.parametrize("sizes", [(4096, 1024, 1024), (300, 77, 13, 8)], ids=["qkv", "ragged"])
+def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, sizes, rng):
+    """Projections of one input in one launch (M = 1) or in sequence (M = 2),
+    with output biases on some of them; ragged sizes exercise the padding
+    between projections."""
+    K = 1024
+    for M in (1, 2):
+        projections, host = [], []
+        x = seeded_problem(M, 8, K, bits, 64, x_dtype, p_dtype, seed=59)[0]
+        for i, n in enumerate(sizes):
+            _, packed, s, b = seeded_problem(M, n, K, bits, 64, x_dtype, p_dtype, seed=60 + 2 * i)
+            parts = [upload(session, a, dtype_of(a)) for a in (packed, s, b)]
+            bias = None
+            if i % 2 == 0:
+                bias = O.bf16_from_f32(rng.standard_normal(n).astype(np.float32))
+                parts.append(upload(session, bias, "bf16"))
+            projections.append(tuple(parts))
+            host.append((packed, s, b, bias))
+        xt = upload(session, x, dtype_of(x))
+        plan = A.grouped_plan(xt, projections, bits=bits, group_size=64)
+        if M == 1 and len(sizes) <= 4:
+            assert plan == f"rocm_quantized_matmul.gemv[grouped:{len(sizes)},bias]", plan
+        else:
+            assert plan.count(";") == len(sizes) - 1, plan
+        outs = A.quantized_matmul_grouped(xt, projections, bits=bits, group_size=64)
+        for out, (packed, s, b, bias), parts in zip(outs, host, projections):
+            expected = O.quantized_matmul(x, packed, s, b, bits, 64)
+            single = A.quantized_matmul(xt, *parts[:3], bits=bits, group_size=64).numpy()
+            if bias is not None:
+                expected = O.add_output_bias(expected, bias)
+                single = O.add_output_bias(single, bias)
+            oracle_close(out.numpy(), expected, x_dtype == "bf16")
+            if M > 1:  # the same kernels one by one: identical results
+                np.testing.assert_array_equal(out.numpy(), single)
+
+
+def test_grouped_validation(session):
+    x, packed, s, b = seeded_problem(1, 64, 256, 4, 64, "bf16", "bf16", seed=3)
+    xt, x2 = upload(session, x, "bf16"), upload(session, x, "bf16")
+    w = tuple(upload(session, a, dtype_of(a)) for a in (packed, s, b))
+    descs = (_native.QmmDesc * 2)()
+    descs[0] = A.ops._descriptor(xt, *w, 4, 64, session.empty("f32", (1, 64)), "auto", "backend_equivalent")
+    descs[1] = A.ops._descriptor(x2, *w, 4, 64, session.empty("f32", (1, 64)), "auto", "backend_equivalent")
+    lib = _native.load()
+    assert lib.affon_rocm_quantized_matmul_grouped(session._handle, descs, None, 2) == _native.INVALID_SHAPE
+    assert "share the input" in _native.last_error()
+    assert lib.affon_rocm_quantized_matmul_grouped(session._handle, descs, None, 0) == _native.INVALID_SHAPE
+    epis = (_native.Epilogue * 1)()
+    epis[0] = A.ops._epilogue(up=w)
+    assert lib.affon_rocm_quantized_matmul_grouped(session._handle, descs, epis, 1) == _native.INVALID_SHAPE
+    assert "output bias" in _native.last_error()

@@ -46,13 +46,36 @@ def test_mul_operand_order_and_bias_either_side():
     assert [s.kind for s in steps_of(source)] == ["silu_gate", "bias"]
 
 
-def test_plain_projections_stay_separate_and_ordered():
+def test_projections_of_one_input_are_grouped_four_at_a_time():
     def body(p):
         h = p.argument("h", TensorSpec.bf16([1, 128]))
-        return [qmm(h, weights(p, n, 64, 128)) for n in ("q", "k", "v")]
+        other = p.argument("other", TensorSpec.bf16([1, 128]))
+        outs = [qmm(h, weights(p, n, 64, 128)) for n in ("q", "k", "v", "a", "b")]
+        outs.append(add(qmm(h, weights(p, "c", 32, 128)), p.argument("c.bias", TensorSpec.f32([32]))))
+        outs.append(qmm(other, weights(p, "o", 64, 128)))
+        return outs
     steps = steps_of(program("qkv", body))
-    assert [s.kind for s in steps] == ["quantized_matmul"] * 3
-    assert [s.node for s in steps] == sorted(s.node for s in steps)
+    assert [s.kind for s in steps] == ["grouped", "grouped", "quantized_matmul"]
+    assert [len(s.members) for s in steps[:2]] == [4, 2]
+    assert [m.kind for m in steps[1].members] == ["quantized_matmul", "bias"]
+    first = [m.node for m in steps[0].members]
+    assert first == sorted(first)
+
+
+def test_grouped_selection_from_specs():
+    from affon_amd.ops import grouped_select_for_specs
+    opts = {"bits": 4, "group_size": 64}
+
+    def member(m, n):
+        return [TensorSpec.bf16([m, 4096]), TensorSpec.u32([n, 512]), TensorSpec.bf16([n, 64]),
+                TensorSpec.bf16([n, 64])]
+    qkv = [member(1, 4096), member(1, 1024), member(1, 1024)]
+    assert grouped_select_for_specs(qkv, opts, "backend_equivalent") == "rocm_quantized_matmul.gemv[grouped:3]"
+    biased = [qkv[0] + [TensorSpec.bf16([4096])], qkv[1] + [TensorSpec.bf16([1024])], qkv[2]]
+    assert grouped_select_for_specs(biased, opts, "backend_equivalent") == "rocm_quantized_matmul.gemv[grouped:3,bias]"
+    batch = [member(2, 4096), member(2, 1024)]
+    assert grouped_select_for_specs(batch, opts, "backend_equivalent") == \
+        "rocm_quantized_matmul.gemv_mfma;rocm_quantized_matmul.gemv_mfma"
 
 
 @pytest.mark.parametrize("case", ["silu_alone", "shared_gate", "gate_is_output", "bias_matrix", "different_inputs",
