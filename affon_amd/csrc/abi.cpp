@@ -531,6 +531,7 @@ struct GroupPlan {
   std::vector<FusedPlan> many;  // more members than one launch takes
   size_t count = 0;
   bool one_launch = false;
+  int one_impl = 0;  // the candidate whose kernel runs the whole group
   const FusedPlan& at(size_t i) const { return count <= affon::kMaxGroup ? members[i] : many[i]; }
 };
 
@@ -558,12 +559,18 @@ int plan_grouped(const affon_rocm_qmm_desc* descs, const affon_rocm_qmm_epilogue
   }
   if (count >= 2 && count <= affon::kMaxGroup) {
     affon::QmmProblem problems[affon::kMaxGroup];
-    bool all_gemv = true;
+    const int impl = plan->members[0].first_c->impl;
+    bool same = true;
     for (size_t i = 0; i < count; ++i) {
       problems[i] = plan->members[i].first;
-      all_gemv = all_gemv && plan->members[i].first_c->impl == AFFON_ROCM_IMPL_GEMV;
+      same = same && plan->members[i].first_c->impl == impl;
     }
-    plan->one_launch = all_gemv && affon::gemv_group_supports(problems, static_cast<int>(count));
+    const int n = static_cast<int>(count);
+    if (same && impl == AFFON_ROCM_IMPL_GEMV)
+      plan->one_launch = affon::gemv_group_supports(problems, n);
+    else if (same && impl == AFFON_ROCM_IMPL_GEMV_MFMA)
+      plan->one_launch = affon::gemv_mfma_group_supports(problems, n);
+    plan->one_impl = impl;
   }
   return AFFON_ROCM_OK;
 }
@@ -604,8 +611,10 @@ int affon_rocm_quantized_matmul_grouped(affon_rocm_session* session, const affon
   if (plan.one_launch) {
     affon::QmmProblem problems[affon::kMaxGroup];
     for (size_t i = 0; i < count; ++i) problems[i] = plan.members[i].first;
-    hipError_t e = affon::gemv_group_launch(problems, static_cast<int>(count), launch);
-    if (e != hipSuccess) return hip_fail(e, "rocm_quantized_matmul.gemv (grouped)");
+    const int n = static_cast<int>(count);
+    hipError_t e = plan.one_impl == AFFON_ROCM_IMPL_GEMV ? affon::gemv_group_launch(problems, n, launch)
+                                                         : affon::gemv_mfma_group_launch(problems, n, launch);
+    if (e != hipSuccess) return hip_fail(e, "grouped quantized_matmul");
     return AFFON_ROCM_OK;
   }
   for (size_t i = 0; i < count; ++i) {

@@ -74,14 +74,12 @@ struct Args {
   const uint8_t* seg_bias[kMaxSegments];  // output bias (element type epi.bias_bf16) or null
 };
 
-// a[seg] for a uniform seg < kMaxSegments, by selects (no dynamic indexing of
-// the kernel argument block).
+// a[seg] for a uniform seg < kMaxSegments, by selects with constant indices
+// (no dynamic indexing of the kernel argument block).
+static_assert(kMaxSegments == 4, "pick spells out four segments");
 template <typename T>
 __device__ __forceinline__ T pick(const T (&a)[kMaxSegments], int seg) {
-  T v = a[0];
-#pragma unroll
-  for (int j = 1; j < kMaxSegments; ++j) v = seg == j ? a[j] : v;
-  return v;
+  return seg == 0 ? a[0] : seg == 1 ? a[1] : seg == 2 ? a[2] : a[3];
 }
 
 template <int BITS>
@@ -386,8 +384,9 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   Epilogue epi = a.epi;
   if constexpr (MODE == kGrouped) {
     int seg = 0;
-#pragma unroll
-    for (int j = 1; j < kMaxSegments; ++j) seg = j < a.segments && n0 >= a.seg_first[j] ? j : seg;
+    if (a.segments > 1 && n0 >= a.seg_first[1]) seg = 1;
+    if (a.segments > 2 && n0 >= a.seg_first[2]) seg = 2;
+    if (a.segments > 3 && n0 >= a.seg_first[3]) seg = 3;
     n0 -= pick(a.seg_first, seg);
     N = pick(a.seg_n, seg);
     W = pick(a.seg_w, seg);

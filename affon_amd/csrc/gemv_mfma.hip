@@ -107,7 +107,8 @@ struct RowBlocks {
   static constexpr int kRows = 16 * kBlocks;           // rows with results
 };
 template <int BITS, typename PT, int XROWS>
-__global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
+  TileArgs a = args;
   constexpr int kXLoads = XROWS / 8;  // activation DMA instructions per step
   using P = Plan<BITS, PT, kXLoads>;
   constexpr int RB = RowBlocks<XROWS>::kBlocks;
@@ -123,9 +124,26 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
   const int r = lane & 15;   // row of the A operand, column of the B operand and output
   const int h = lane >> 4;   // lane quarter
 
-  const int nb_n = (a.N + kCols - 1) / kCols;
+  const int nb_n = a.seg.count > 0 ? a.seg.total_tiles : (a.N + kCols - 1) / kCols;
   int tile, split;
   work_unit(nb_n, a.splits, &tile, &split);
+  // A grouped launch: the workgroup's projection (all uniform), and where
+  // its columns sit in the partial planes.
+  int col_base = 0;
+  int64_t pstride = a.N;
+  if (a.seg.count > 0) {
+    const int k = seg_of(a.seg, a.seg.first_tile, tile);
+    tile -= seg_pick(a.seg.first_tile, k);
+    col_base = seg_pick(a.seg.col_base, k);
+    pstride = a.seg.total_n;
+    a.w = seg_pick(a.seg.w, k);
+    a.s = seg_pick(a.seg.s, k);
+    a.b = seg_pick(a.seg.b, k);
+    a.out = seg_pick(a.seg.out, k);
+    a.N = seg_pick(a.seg.n, k);
+    a.epi.bias = seg_pick(a.seg.bias, k);
+    a.epi.kind = a.epi.bias != nullptr ? kEpiBias : kEpiNone;
+  }
   const int n0 = tile * kCols;
   // K range of this wave, in whole 4-step chunks: chunks [c0, c1) of the
   // workgroup's range, itself chunks [split*C/S, (split+1)*C/S) of K.
@@ -257,25 +275,24 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) ysum(wave)[(16 * rb + 4 * h + i) * kCols + 16 * ct + r] = y[rb][ct][i];
   __syncthreads();
-  float* dst = a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N;
+  float* dst = a.partial + split * static_cast<int64_t>(a.M) * pstride;
 #pragma unroll
   for (int e = 0; e < kRows * kCols / kThreads; ++e) {
     const int o = e * kThreads + tid;
     const int row = o / kCols, col = n0 + o % kCols;
     if (row < a.M && col < a.N) {
       const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
-      const int64_t i = static_cast<int64_t>(row) * a.N + col;
       if (a.splits == 1)
-        store_output(a.epi, dst, i, col, v);
+        store_output(a.epi, a.out, static_cast<int64_t>(row) * a.N + col, col, v);
       else
-        dst[i] = v;
+        dst[static_cast<int64_t>(row) * pstride + col_base + col] = v;
     }
   }
 }
 
 template <int BITS, typename PT>
 hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
-  const int tiles = (args.N + kCols - 1) / kCols;
+  const int tiles = args.seg.count > 0 ? args.seg.total_tiles : (args.N + kCols - 1) / kCols;
   const dim3 grid(tiles * args.splits);
   if (args.M <= 8)
     hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 8>), grid, dim3(kThreads), 0, stream, args);
@@ -317,6 +334,10 @@ bool gemv_mfma_supports(const QmmProblem& p) {
   return true;
 }
 
+namespace {
+hipError_t tiled_launch(const QmmProblem& p, const QmmProblem* group, int count, const Launch& l);
+}  // namespace
+
 hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
   // M <= 4: a virtual-row kernel (packed words straight into the B operand,
   // no LDS for weights); larger batches: the LDS-tiled kernel.
@@ -332,6 +353,14 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
     default:
       break;
   }
+  return tiled_launch(p, nullptr, 0, l);
+}
+
+namespace {
+
+// The LDS-tiled kernel on one problem, or (count > 0) on a group of
+// problems that share the activations, as one grouped launch.
+hipError_t tiled_launch(const QmmProblem& p, const QmmProblem* group, int count, const Launch& l) {
   TileArgs a;
   a.x = reinterpret_cast<const uint16_t*>(p.x);
   a.xs0 = p.xs0;
@@ -348,7 +377,31 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
   a.K = static_cast<int>(p.K);
   a.group_shift = 0;
   while ((int64_t(32) << a.group_shift) < p.group) ++a.group_shift;
-  const int tiles = static_cast<int>((p.N + kCols - 1) / kCols);
+  int tiles = static_cast<int>((p.N + kCols - 1) / kCols);
+  int64_t columns = p.N;
+  if (count > 0) {
+    a.seg.count = count;
+    tiles = 0;
+    columns = 0;
+    for (int k = 0; k < kMaxSegments; ++k) {
+      const bool used = k < count;
+      a.seg.first_tile[k] = tiles;
+      a.seg.col_base[k] = static_cast<int>(columns);
+      a.seg.n[k] = used ? static_cast<int>(group[k].N) : 0;
+      a.seg.w[k] = used ? group[k].w : nullptr;
+      a.seg.s[k] = used ? group[k].s : nullptr;
+      a.seg.b[k] = used ? group[k].b : nullptr;
+      a.seg.out[k] = used ? group[k].out : nullptr;
+      a.seg.bias[k] = used && group[k].epi.kind == kEpiBias ? group[k].epi.bias : nullptr;
+      if (used) {
+        if (group[k].epi.kind == kEpiBias) a.epi.bias_bf16 = group[k].epi.bias_bf16;
+        tiles += static_cast<int>((group[k].N + kCols - 1) / kCols);
+        columns += group[k].N;
+      }
+    }
+    a.seg.total_tiles = tiles;
+    a.seg.total_n = static_cast<int>(columns);
+  }
   const int chunks = static_cast<int>(p.K / (4 * kBK));
   a.splits = 1;
   a.split_steps = 0;  // ranges are computed per workgroup from K and splits
@@ -359,7 +412,7 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
   if (l.workspace != nullptr)
     while (splits < 8 && tiles * splits < device_cus() * 3 / 4 && chunks >= 2 * kWaves * 2 * splits) splits *= 2;
   if (splits > 1) {
-    if (auto* w = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * p.N * 4))) {
+    if (auto* w = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * columns * 4))) {
       a.splits = splits;
       a.partial = w;
     }
@@ -370,6 +423,30 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
     case 4: return bf16p ? launch_typed<4, BF16>(a, l.stream) : launch_typed<4, F32>(a, l.stream);
     default: return bf16p ? launch_typed<8, BF16>(a, l.stream) : launch_typed<8, F32>(a, l.stream);
   }
+}
+
+}  // namespace
+
+bool gemv_mfma_group_supports(const QmmProblem* group, int count) {
+  if (count < 2 || count > kMaxGroup || count > kMaxSegments) return false;
+  const QmmProblem& p = group[0];
+  for (int i = 0; i < count; ++i) {
+    const QmmProblem& q = group[i];
+    if (!gemv_mfma_supports(q) || vrow_layout(q) != 0) return false;  // the LDS-tiled kernel only
+    if (q.epi.kind != kEpiNone && q.epi.kind != kEpiBias) return false;
+    if (q.x != p.x || q.xs0 != p.xs0 || q.M != p.M || q.K != p.K || q.bits != p.bits || q.group != p.group ||
+        q.p_dtype != p.p_dtype || q.ws0 != p.ws0 || q.ss0 != p.ss0 || q.bs0 != p.bs0)
+      return false;
+    for (int j = 0; j < count; ++j)
+      if (q.epi.kind == kEpiBias && group[j].epi.kind == kEpiBias && group[j].epi.bias_bf16 != q.epi.bias_bf16)
+        return false;
+  }
+  return true;
+}
+
+hipError_t gemv_mfma_group_launch(const QmmProblem* group, int count, const Launch& l) {
+  if (!gemv_mfma_group_supports(group, count)) return hipErrorInvalidValue;
+  return tiled_launch(group[0], group, count, l);
 }
 
 }  // namespace affon

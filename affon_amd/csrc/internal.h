@@ -73,6 +73,11 @@ hipError_t gemv_group_launch(const QmmProblem* group, int count, const Launch& l
 
 bool gemv_mfma_supports(const QmmProblem& p);
 hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l);
+// Grouped launch of 2..4 problems on the LDS-tiled kernel (decode batches
+// the virtual-row kernels do not take) that share the activations, bits,
+// group size, dtypes and strides.
+bool gemv_mfma_group_supports(const QmmProblem* group, int count);
+hipError_t gemv_mfma_group_launch(const QmmProblem* group, int count, const Launch& l);
 
 bool mfma_supports(const QmmProblem& p);
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l);

@@ -25,6 +25,41 @@ constexpr int kWaves = 4;      // waves per workgroup, side by side along N (64 
 constexpr int kThreads = 64 * kWaves;
 constexpr int kStages = 4;     // LDS ring depth (steps)
 
+constexpr int kMaxSegments = 4;
+
+// A grouped tiled launch: up to kMaxSegments projections of one activation
+// tensor (same K, group size, dtypes and strides). Segment j owns the
+// launch's tiles [first_tile[j], first_tile[j+1]) and columns [col_base[j],
+// col_base[j] + n[j]) of the launch's column space, in which the split-K
+// partial planes are laid out (row stride total_n).
+struct Segments {
+  int count = 0;  // 0: an ordinary launch (the operands in TileArgs)
+  int total_tiles, total_n;
+  int first_tile[kMaxSegments], col_base[kMaxSegments], n[kMaxSegments];
+  const uint32_t* w[kMaxSegments];
+  const uint8_t* s[kMaxSegments];
+  const uint8_t* b[kMaxSegments];
+  float* out[kMaxSegments];
+  const uint8_t* bias[kMaxSegments];  // output bias (element type epi.bias_bf16) or null
+};
+
+// v[k] for a uniform k < kMaxSegments, by selects with constant indices (so
+// that a copy of the arguments stays in scalar registers).
+static_assert(kMaxSegments == 4, "seg_pick and seg_of spell out four segments");
+template <typename T>
+__device__ __forceinline__ T seg_pick(const T (&v)[kMaxSegments], int k) {
+  return k == 0 ? v[0] : k == 1 ? v[1] : k == 2 ? v[2] : v[3];
+}
+
+// The segment holding launch tile (or column) t, given each segment's first.
+__device__ __forceinline__ int seg_of(const Segments& g, const int (&first)[kMaxSegments], int t) {
+  int k = 0;
+  if (g.count > 1 && t >= first[1]) k = 1;
+  if (g.count > 2 && t >= first[2]) k = 2;
+  if (g.count > 3 && t >= first[3]) k = 3;
+  return k;
+}
+
 // Operands of one tiled launch.
 struct TileArgs {
   const uint16_t* x;  // bf16 [M, K], row stride xs0 elements
@@ -44,6 +79,7 @@ struct TileArgs {
   int splits, split_steps;
   float* partial;
   Epilogue epi;  // applied where the output is stored (the reduction when splits > 1)
+  Segments seg;
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {

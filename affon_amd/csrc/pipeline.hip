@@ -9,11 +9,29 @@ namespace {
 // out[i] = sum of the K ranges' partial sums, added in range order (the same
 // result on every run), then the output epilogue. Four outputs per thread;
 // `count` = M*N, `n` = N; `vec` when count % 4 == 0 and out is 16-byte
-// aligned (partial always is).
+// aligned (partial always is). A grouped launch's partials span all its
+// segments' columns (row stride n = total columns); each sum goes to its
+// segment's output.
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* partial, float* out, int64_t count,
-                                                              int64_t n, int splits, int vec, Epilogue epi) {
+                                                              int64_t n, int splits, int vec, Epilogue epi,
+                                                              Segments seg) {
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i >= count) return;
+  if (seg.count > 0) {
+    for (int64_t j = i; j < i + 4 && j < count; ++j) {
+      float sum = partial[j];
+      for (int r = 1; r < splits; ++r) sum += partial[r * count + j];
+      const int64_t row = j / n;
+      const int c = static_cast<int>(j - row * n);
+      const int k = seg_of(seg, seg.col_base, c);
+      const int col = c - seg_pick(seg.col_base, k);
+      Epilogue e = epi;
+      e.bias = seg_pick(seg.bias, k);
+      e.kind = e.bias != nullptr ? kEpiBias : kEpiNone;
+      store_output(e, seg_pick(seg.out, k), row * seg_pick(seg.n, k) + col, col, sum);
+    }
+    return;
+  }
   if (vec) {
     f32x4_t sum = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + i));
     for (int r = 1; r < splits; ++r) sum += __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(partial + r * count + i));
@@ -64,11 +82,12 @@ int choose_splits(int tiles, int steps) {
 
 
 hipError_t launch_reduce(const TileArgs& args, hipStream_t stream) {
-  const int64_t count = static_cast<int64_t>(args.M) * args.N;
+  const int64_t n = args.seg.count > 0 ? args.seg.total_n : args.N;
+  const int64_t count = static_cast<int64_t>(args.M) * n;
   const int64_t blocks = (count + 1023) / 1024;
-  const int vec = count % 4 == 0 && reinterpret_cast<uintptr_t>(args.out) % 16 == 0;
+  const int vec = args.seg.count == 0 && count % 4 == 0 && reinterpret_cast<uintptr_t>(args.out) % 16 == 0;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     args.partial, args.out, count, static_cast<int64_t>(args.N), args.splits, vec, args.epi);
+                     args.partial, args.out, count, n, args.splits, vec, args.epi, args.seg);
   return hipGetLastError();
 }
 

@@ -179,8 +179,10 @@ int affon_rocm_quantized_matmul_fused_select(const affon_rocm_qmm_desc* desc, co
  * in packed, scales, biases and output; input, bits, group_size,
  * implementation and numerical_policy are shared. epilogues is null or holds
  * count entries, each AFFON_ROCM_EPILOGUE_NONE or _BIAS. Results equal count
- * separate calls. When the M = 1 gemv kernel is selected for every call and
- * count <= 4 (with equal strides) they run as one launch. */
+ * separate calls. They run as one launch when count <= 4, the strides are
+ * equal and every call selects the same kernel that takes groups: the M = 1
+ * gemv kernel, or the LDS-tiled gemv_mfma kernel (bf16 decode batches the
+ * virtual-row kernels do not take). */
 int affon_rocm_quantized_matmul_grouped(affon_rocm_session* session, const affon_rocm_qmm_desc* descs,
                                         const affon_rocm_qmm_epilogue* epilogues, size_t count);
 

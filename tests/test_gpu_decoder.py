@@ -82,8 +82,9 @@ def test_decoder_block_programs_against_oracle(session, tmp_path, M):
     impl = attention_nodes[0]["implementation_id"]
     if M == 1:
         assert impl == "rocm_quantized_matmul.gemv[grouped:3,bias]", impl
-    else:
-        assert impl.count(";") == 2 and impl.endswith("[bias]"), impl
+    else:  # one grouped launch on the LDS-tiled kernel, or three launches
+        assert impl == "rocm_quantized_matmul.gemv_mfma[grouped:3,bias]" or \
+            (impl.count(";") == 2 and impl.endswith("[bias]")), impl
 
 
 def test_decoder_block_rejects_mismatched_layers(session, tmp_path):

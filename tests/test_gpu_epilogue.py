@@ -205,11 +205,12 @@ def test_epilogue_validation_leaves_output_untouched(session):
 @pytest.mark.parametrize("x_dtype,p_dtype,bits", [("bf16", "bf16", 4), ("f32", "f32", 8), ("bf16", "f32", 2)])
 @pytest.mark.parametrize("sizes", [(4096, 1024, 1024), (300, 77, 13, 8)], ids=["qkv", "ragged"])
 def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, sizes, rng):
-    """Projections of one input in one launch (M = 1) or in sequence (M = 2),
-    with output biases on some of them; ragged sizes exercise the padding
-    between projections."""
+    """Projections of one input in one launch (M = 1: the gemv kernel; M = 16
+    with bf16 activations: the LDS-tiled gemv_mfma kernel, whose split-K
+    partials span all projections) or in sequence (M = 2), with output biases
+    on some of them; ragged sizes exercise the padding between projections."""
     K = 1024
-    for M in (1, 2):
+    for M in (1, 2, 16):
         projections, host = [], []
         x = seeded_problem(M, 8, K, bits, 64, x_dtype, p_dtype, seed=59)[0]
         for i, n in enumerate(sizes):
@@ -223,8 +224,10 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, siz
             host.append((packed, s, b, bias))
         xt = upload(session, x, dtype_of(x))
         plan = A.grouped_plan(xt, projections, bits=bits, group_size=64)
-        if M == 1 and len(sizes) <= 4:
-            assert plan == f"rocm_quantized_matmul.gemv[grouped:{len(sizes)},bias]", plan
+        one_launch = M == 1 or (M == 16 and x_dtype == "bf16")
+        if one_launch:
+            kernel = "gemv" if M == 1 else "gemv_mfma"
+            assert plan == f"rocm_quantized_matmul.{kernel}[grouped:{len(sizes)},bias]", plan
         else:
             assert plan.count(";") == len(sizes) - 1, plan
         outs = A.quantized_matmul_grouped(xt, projections, bits=bits, group_size=64)
@@ -235,7 +238,7 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, siz
                 expected = O.add_output_bias(expected, bias)
                 single = O.add_output_bias(single, bias)
             oracle_close(out.numpy(), expected, x_dtype == "bf16")
-            if M > 1:  # the same kernels one by one: identical results
+            if not one_launch:  # the same kernels one by one: identical results
                 np.testing.assert_array_equal(out.numpy(), single)
 
 

@@ -73,9 +73,11 @@ def test_grouped_selection_from_specs():
     assert grouped_select_for_specs(qkv, opts, "backend_equivalent") == "rocm_quantized_matmul.gemv[grouped:3]"
     biased = [qkv[0] + [TensorSpec.bf16([4096])], qkv[1] + [TensorSpec.bf16([1024])], qkv[2]]
     assert grouped_select_for_specs(biased, opts, "backend_equivalent") == "rocm_quantized_matmul.gemv[grouped:3,bias]"
-    batch = [member(2, 4096), member(2, 1024)]
+    batch = [member(2, 4096), member(2, 1024)]  # the virtual-row kernels take no groups
     assert grouped_select_for_specs(batch, opts, "backend_equivalent") == \
         "rocm_quantized_matmul.gemv_mfma;rocm_quantized_matmul.gemv_mfma"
+    batch = [member(32, 4096), member(32, 1024), member(32, 1024)]  # the LDS-tiled kernel does
+    assert grouped_select_for_specs(batch, opts, "backend_equivalent") == "rocm_quantized_matmul.gemv_mfma[grouped:3]"
 
 
 @pytest.mark.parametrize("case", ["silu_alone", "shared_gate", "gate_is_output", "bias_matrix", "different_inputs",
