@@ -5,13 +5,13 @@ The product is the native library ``libaffon_rocm.so`` (C ABI in
 reference's ``affon:ops`` / Session surface over that ABI.
 """
 from .core import Executable, FormalTensor, Program, Session, Tensor, TensorSpec, program
-from .ops import (dequantize, fused_plan, grouped_plan, quantize, quantized_linear, quantized_matmul,
-                  quantized_matmul_grouped, quantized_matmul_into, quantized_silu_gate, selected_implementation, slice,
-                  transpose)
+from .ops import (add, dequantize, fused_plan, grouped_plan, index_select, mul, quantize, quantized_linear,
+                  quantized_matmul, quantized_matmul_grouped, quantized_matmul_into, quantized_silu_gate, rms_norm,
+                  selected_implementation, silu, slice, softmax, transpose)
 
 __all__ = [
     "Executable", "FormalTensor", "Program", "Session", "Tensor", "TensorSpec", "program",
-    "dequantize", "fused_plan", "grouped_plan", "quantize", "quantized_linear", "quantized_matmul",
-    "quantized_matmul_grouped", "quantized_matmul_into", "quantized_silu_gate", "selected_implementation", "slice",
-    "transpose",
+    "add", "dequantize", "fused_plan", "grouped_plan", "index_select", "mul", "quantize", "quantized_linear",
+    "quantized_matmul", "quantized_matmul_grouped", "quantized_matmul_into", "quantized_silu_gate", "rms_norm",
+    "selected_implementation", "silu", "slice", "softmax", "transpose",
 ]

@@ -91,6 +91,10 @@ SIGNATURES = {
                                     c_void_p, c_void_p, c_void_p, c_int32]),
     "affon_rocm_dequantize": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64,
                                       c_uint32, c_uint32, c_void_p, c_int32]),
+    "affon_rocm_rms_norm": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_int64, ctypes.c_float, c_void_p]),
+    "affon_rocm_softmax": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_int64, c_void_p]),
+    "affon_rocm_index_select": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p, c_int64,
+                                        c_void_p]),
 }
 
 _LIB: ctypes.CDLL | None = None

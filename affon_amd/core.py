@@ -29,10 +29,10 @@ import numpy as np
 
 from . import _native
 
-DTYPES = ("bf16", "f32", "u32")
+DTYPES = ("bf16", "f32", "u32", "i64")
 _NATIVE_DTYPE = {"f32": _native.F32, "bf16": _native.BF16, "u32": _native.U32}
-_ITEMSIZE = {"f32": 4, "bf16": 2, "u32": 4}
-_STORAGE = {"f32": np.float32, "bf16": np.uint16, "u32": np.uint32}
+_ITEMSIZE = {"f32": 4, "bf16": 2, "u32": 4, "i64": 8}
+_STORAGE = {"f32": np.float32, "bf16": np.uint16, "u32": np.uint32, "i64": np.int64}
 
 COMPILE_OPTION_VALUES = {
     "optimizationLevel": ("none", "safe"),
@@ -60,6 +60,8 @@ def host_storage(values: Any, dtype: str) -> np.ndarray:
     first, then bf16 rounding (src/js/compute/native.zig:1166-1177)."""
     if dtype == "u32":
         return np.ascontiguousarray(np.asarray(values, dtype=np.float64).astype(np.uint64).astype(np.uint32))
+    if dtype == "i64":
+        return np.ascontiguousarray(np.asarray(values, dtype=np.int64))
     f32 = np.ascontiguousarray(np.asarray(values, dtype=np.float64).astype(np.float32))
     return bf16_bits(f32) if dtype == "bf16" else f32
 
@@ -103,6 +105,10 @@ class TensorSpec:
     def u32(shape: Sequence[int]) -> "TensorSpec":
         return TensorSpec("u32", tuple(int(d) for d in shape))
 
+    @staticmethod
+    def i64(shape: Sequence[int]) -> "TensorSpec":
+        return TensorSpec("i64", tuple(int(d) for d in shape))
+
 
 class Tensor:
     """An evaluated device tensor (or a view of one) owned by a Session."""
@@ -127,8 +133,8 @@ class Tensor:
 
     def view(self) -> _native.View:
         self._check_live()
-        if len(self.shape) != 2:
-            raise TypeError("rank-two tensor required")
+        if len(self.shape) != 2 or self.dtype not in _NATIVE_DTYPE:
+            raise TypeError("rank-two f32/bf16/u32 tensor required")
         return _native.View(self._buffer.ptr, self._buffer.nbytes, self.offset * _ITEMSIZE[self.dtype],
                             (ctypes.c_int64 * 2)(*self.shape), (ctypes.c_int64 * 2)(*self.strides),
                             _NATIVE_DTYPE[self.dtype])
@@ -371,6 +377,8 @@ class Executable:
         policy = self.options["numericalPolicy"]
         if step.kind == "quantized_matmul":
             return self._ops.select_for_specs(specs, step.options, policy)
+        if step.kind in ("rms_norm", "softmax", "index_select"):
+            return f"rocm_{step.kind}"
         if step.kind == "grouped":
             members = [[self.program.nodes[i]["spec"] for i in m.operands] for m in step.members]
             return self._ops.grouped_select_for_specs(members, step.options, policy)
@@ -378,7 +386,8 @@ class Executable:
 
     def explain(self) -> dict[str, Any]:
         names = {"quantized_matmul": "quantized_matmul", "bias": "quantized_matmul+add",
-                 "silu_gate": "quantized_matmul+silu+quantized_matmul+mul"}
+                 "silu_gate": "quantized_matmul+silu+quantized_matmul+mul", "rms_norm": "rms_norm",
+                 "softmax": "softmax", "index_select": "index_select"}
 
         def op(step):
             if step.kind == "grouped":
@@ -405,6 +414,15 @@ class Executable:
         policy = self.options["numericalPolicy"]
         for step in self._steps:
             operands = [values[i] for i in step.operands]
+            if step.kind == "rms_norm":
+                values[step.node] = self._ops._run_rms_norm(operands[0], step.options["epsilon"])
+                continue
+            if step.kind == "softmax":
+                values[step.node] = self._ops._run_softmax(operands[0])
+                continue
+            if step.kind == "index_select":
+                values[step.node] = self._ops._run_index_select(operands[0], step.options["axis"], operands[1])
+                continue
             bits, group = step.options["bits"], step.options["group_size"]
             if step.kind == "quantized_matmul":
                 values[step.node] = self._ops._run_quantized_matmul(*operands, bits, group, policy=policy)

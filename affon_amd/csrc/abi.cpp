@@ -712,6 +712,57 @@ int affon_rocm_dequantize(affon_rocm_session* session, const uint32_t* packed, c
   return AFFON_ROCM_OK;
 }
 
+static int check_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, const void* out, const char* op) {
+  if (!is_float_dtype(dtype)) return fail(AFFON_ROCM_INVALID_SHAPE, "%s requires an f32 or bf16 tensor", op);
+  if (rows <= 0 || cols <= 0) return fail(AFFON_ROCM_INVALID_SHAPE, "%s requires a non-empty rank-two tensor", op);
+  uint64_t count = 0;
+  if (!mul_ok(static_cast<uint64_t>(rows), static_cast<uint64_t>(cols), &count) || count > (uint64_t(1) << 40))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "%s size overflows", op);
+  if (x == nullptr || out == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "%s buffer is null", op);
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_rms_norm(affon_rocm_session* session, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                        float epsilon, void* out) {
+  clear_error();
+  int status = check_rows(x, dtype, rows, cols, out, "rms_norm");
+  if (status != AFFON_ROCM_OK) return status;
+  if (!(epsilon >= 0.0f) || epsilon == std::numeric_limits<float>::infinity())
+    return fail(AFFON_ROCM_INVALID_SHAPE, "rms_norm epsilon must be finite and non-negative");
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::rms_norm_launch(x, dtype, rows, cols, epsilon, out, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "rms_norm");
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_softmax(affon_rocm_session* session, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                       void* out) {
+  clear_error();
+  int status = check_rows(x, dtype, rows, cols, out, "softmax");
+  if (status != AFFON_ROCM_OK) return status;
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::softmax_launch(x, dtype, rows, cols, out, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "softmax");
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_index_select(affon_rocm_session* session, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                            int32_t axis, const int64_t* index, int64_t count, void* out) {
+  clear_error();
+  int status = check_rows(x, dtype, rows, cols, out, "index_select");
+  if (status != AFFON_ROCM_OK) return status;
+  if (axis != 0 && axis != 1) return fail(AFFON_ROCM_INVALID_SHAPE, "index_select axis must be 0 or 1");
+  if (count <= 0 || index == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "index_select requires indices");
+  uint64_t total = 0;
+  if (!mul_ok(static_cast<uint64_t>(count), static_cast<uint64_t>(axis == 0 ? cols : rows), &total) ||
+      total > (uint64_t(1) << 40))
+    return fail(AFFON_ROCM_INVALID_SHAPE, "index_select size overflows");
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::index_select_launch(x, dtype, rows, cols, axis, index, count, out, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "index_select");
+  return AFFON_ROCM_OK;
+}
+
 // ---- host-pointer drop-in for compute_core_run_quantized_matmul_f32 ----
 
 namespace {

@@ -85,6 +85,11 @@ hipError_t mfma_launch(const QmmProblem& p, const Launch& l);
 hipError_t quantize_launch(const void* weights, int weight_dtype, int64_t rows, int64_t columns,
                            int bits, int64_t group, uint32_t* packed, void* scales, void* biases,
                            int param_dtype, hipStream_t stream);
+hipError_t rms_norm_launch(const void* x, int dtype, int64_t rows, int64_t cols, float epsilon, void* out,
+                           hipStream_t stream);
+hipError_t softmax_launch(const void* x, int dtype, int64_t rows, int64_t cols, void* out, hipStream_t stream);
+hipError_t index_select_launch(const void* x, int dtype, int64_t rows, int64_t cols, int axis, const int64_t* index,
+                               int64_t count, void* out, hipStream_t stream);
 hipError_t dequantize_launch(const uint32_t* packed, const void* scales, const void* biases,
                              int param_dtype, int64_t rows, int64_t columns, int bits, int64_t group,
                              void* out, int out_dtype, hipStream_t stream);

@@ -28,6 +28,8 @@ from dataclasses import dataclass, field
 from typing import Any, Sequence
 
 ELEMENTWISE = ("add", "mul", "silu")
+# Ops with a rocm kernel of their own: one step each.
+STANDALONE = ("rms_norm", "softmax", "index_select")
 
 
 @dataclass
@@ -88,6 +90,9 @@ def lower(nodes: Sequence[dict[str, Any]], outputs: Sequence[int]) -> list[Step]
         i = n["id"]
         if n["op"] == "quantized_matmul":
             pending[i] = Step("quantized_matmul", i, list(n["operands"]), dict(n["options"]))
+            continue
+        if n["op"] in STANDALONE:
+            steps.append(Step(n["op"], i, list(n["operands"]), dict(n["options"])))
             continue
         if n["op"] == "silu":
             (src,) = n["operands"]

@@ -26,6 +26,8 @@ from __future__ import annotations
 import ctypes
 from typing import Any, Mapping, Sequence
 
+import numpy as np
+
 from . import _native
 from .core import FormalTensor, Tensor, TensorSpec, policy_code
 
@@ -505,3 +507,103 @@ def slice(t: Tensor, ranges: Sequence[Mapping[str, int]]) -> Tensor:  # noqa: A0
         strides.append(stride * step)
         offset += start * stride
     return Tensor(t.session, t._buffer, t.dtype, shape, strides, offset)
+
+
+# ---- the other ops of a decode step (rms_norm, softmax, index_select) ----
+# src/js/ops.ts:97,99,119; catalogued for a decode step in
+# test/parity/catalogs/cuda-apertus-decode-ops.json:1-26. Rank-two f32/bf16
+# tensors; rms_norm and softmax along the last axis.
+
+def _last_axis(name: str, x: Any, axis: Any) -> None:
+    if not isinstance(axis, int) or isinstance(axis, bool):
+        raise TypeError(f"{name} axis must be an integer")
+    rank = len(x.shape)
+    if rank != 2:
+        raise TypeError(f"{name} on rocm requires a rank-two tensor")
+    if axis not in (-1, rank - 1):
+        raise TypeError(f"{name} on rocm runs along the last axis")
+    if x.dtype not in ("f32", "bf16"):
+        raise TypeError(f"{name} requires an f32 or bf16 tensor")
+
+
+def _contiguous_input(name: str, x: Tensor) -> None:
+    if not x.is_contiguous():
+        raise TypeError(f"{name} on rocm requires a contiguous tensor")
+
+
+def rms_norm(x: Any, axis: int, epsilon: float = 1e-5) -> Any:
+    """x / sqrt(mean(x^2 along axis) + epsilon), computed in f32."""
+    _last_axis("rms_norm", x, axis)
+    epsilon = float(epsilon)
+    if not np.isfinite(epsilon) or epsilon < 0:
+        raise TypeError("rms_norm epsilon must be finite and non-negative")
+    if isinstance(x, FormalTensor):
+        return x.builder.emit("rms_norm", (x,), x.spec, {"axis": axis, "epsilon": epsilon})
+    if not isinstance(x, Tensor):
+        raise TypeError("rms_norm requires a tensor")
+    return _run_rms_norm(x, epsilon)
+
+
+def _run_rms_norm(x: Tensor, epsilon: float) -> Tensor:
+    _contiguous_input("rms_norm", x)
+    out = x.session.empty(x.dtype, x.shape)
+    code = {"f32": _native.F32, "bf16": _native.BF16}[x.dtype]
+    _native.check(_native.load().affon_rocm_rms_norm(x.session._handle, x.data_ptr, code, x.shape[0], x.shape[1],
+                                                     epsilon, out.data_ptr), "Program execution failed")
+    return out
+
+
+def softmax(x: Any, axis: int) -> Any:
+    """exp(x - max) / sum(exp(x - max)) along axis, computed in f32."""
+    _last_axis("softmax", x, axis)
+    if isinstance(x, FormalTensor):
+        return x.builder.emit("softmax", (x,), x.spec, {"axis": axis})
+    if not isinstance(x, Tensor):
+        raise TypeError("softmax requires a tensor")
+    return _run_softmax(x)
+
+
+def _run_softmax(x: Tensor) -> Tensor:
+    _contiguous_input("softmax", x)
+    out = x.session.empty(x.dtype, x.shape)
+    code = {"f32": _native.F32, "bf16": _native.BF16}[x.dtype]
+    _native.check(_native.load().affon_rocm_softmax(x.session._handle, x.data_ptr, code, x.shape[0], x.shape[1],
+                                                    out.data_ptr), "Program execution failed")
+    return out
+
+
+def index_select(x: Any, axis: int, indices: Any) -> Any:
+    """Rows (axis 0) or columns (axis 1) of x at i64 indices; indices outside
+    the axis select zeros."""
+    if isinstance(x, FormalTensor) != isinstance(indices, FormalTensor):
+        raise TypeError("index_select cannot mix formal and evaluated tensors")
+    if not isinstance(axis, int) or isinstance(axis, bool) or len(x.shape) != 2 or axis not in (0, 1, -1, -2):
+        raise TypeError("index_select on rocm takes a rank-two tensor and axis 0 or 1")
+    axis = axis % 2
+    if x.dtype not in ("f32", "bf16"):
+        raise TypeError("index_select requires an f32 or bf16 tensor")
+    if indices.dtype != "i64" or len(indices.shape) != 1 or indices.shape[0] <= 0:
+        raise TypeError("index_select indices must be a non-empty rank-one i64 tensor")
+    count = indices.shape[0]
+    shape = (count, x.shape[1]) if axis == 0 else (x.shape[0], count)
+    if isinstance(x, FormalTensor):
+        if x.builder is not indices.builder:
+            raise TypeError("index_select operands must belong to the same Program")
+        return x.builder.emit("index_select", (x, indices), TensorSpec(x.dtype, shape), {"axis": axis})
+    if not isinstance(x, Tensor) or not isinstance(indices, Tensor):
+        raise TypeError("index_select requires tensors")
+    if indices.session is not x.session:
+        raise TypeError("index_select operands must belong to the same Session")
+    return _run_index_select(x, axis, indices)
+
+
+def _run_index_select(x: Tensor, axis: int, indices: Tensor) -> Tensor:
+    _contiguous_input("index_select", x)
+    _contiguous_input("index_select", indices)
+    count = indices.shape[0]
+    out = x.session.empty(x.dtype, (count, x.shape[1]) if axis == 0 else (x.shape[0], count))
+    code = {"f32": _native.F32, "bf16": _native.BF16}[x.dtype]
+    _native.check(_native.load().affon_rocm_index_select(x.session._handle, x.data_ptr, code, x.shape[0], x.shape[1],
+                                                         axis, indices.data_ptr, count, out.data_ptr),
+                  "Program execution failed")
+    return out

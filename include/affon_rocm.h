@@ -233,6 +233,30 @@ int affon_rocm_dequantize(affon_rocm_session* session, const uint32_t* packed, c
                           const void* biases, int32_t param_dtype, int64_t rows, int64_t columns,
                           uint32_t bits, uint32_t group_size, void* out, int32_t out_dtype);
 
+/* ---- the other ops of a decode step (test/parity/catalogs/cuda-apertus-decode-ops.json:1-26) ----
+ * Contiguous rank-two device tensors [rows, cols] of dtype f32 or bf16;
+ * arithmetic in f32, bf16 results rounded to nearest even; the result has
+ * the input's dtype and shape (index_select: the selected shape). */
+
+/* rms_norm along the last axis: out[r,c] = x[r,c] / sqrt(mean_c(x[r,:]^2) + epsilon).
+ * Replaces compute.Session.run for OpTag.rms_norm (src/js/compute/native.zig:739;
+ * op src/js/ops.ts:99, epsilon default 1e-5). */
+int affon_rocm_rms_norm(affon_rocm_session* session, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                        float epsilon, void* out);
+
+/* softmax along the last axis: out[r,c] = exp(x[r,c] - max_r) / sum_c exp(x[r,c] - max_r).
+ * Replaces compute.Session.run for OpTag.softmax (native.zig:739; op src/js/ops.ts:97). */
+int affon_rocm_softmax(affon_rocm_session* session, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                       void* out);
+
+/* index_select along axis 0 (out[i,:] = x[index[i],:], out [count, cols]) or
+ * axis 1 (out[:,i] = x[:,index[i]], out [rows, count]) with count device i64
+ * indices; an index outside [0, size) selects zeros. Replaces
+ * compute.Session.run for OpTag.index_select (native.zig:739; op
+ * src/js/ops.ts:119; zero fill test/parity/reference/probe-capabilities.py:150-153). */
+int affon_rocm_index_select(affon_rocm_session* session, const void* x, int32_t dtype, int64_t rows, int64_t cols,
+                            int32_t axis, const int64_t* index, int64_t count, void* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -160,3 +160,51 @@ def silu(g: np.ndarray) -> np.ndarray:
 def silu_gate(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     """``mul(silu(gate), up)`` in f32 (model.ts:82)."""
     return (silu(gate) * np.asarray(up, dtype=np.float32)).astype(np.float32)
+
+
+# ---- the other ops of a decode step (rms_norm, softmax, index_select) ----
+# Restated from the reference's capability-probe oracle
+# (test/parity/reference/probe-capabilities.py): values widened to f64, the
+# op computed in f64, the result rounded to the input's dtype (f32, or bf16
+# round-to-nearest-even as its `rounded`, :111-116).
+
+def _widen(x: np.ndarray) -> np.ndarray:
+    return f32_from_bf16(x).astype(np.float64) if x.dtype == np.uint16 else np.asarray(x, dtype=np.float64)
+
+
+def _narrow(values: np.ndarray, like: np.ndarray) -> np.ndarray:
+    f32 = np.asarray(values, dtype=np.float64).astype(np.float32)
+    return bf16_from_f32(f32) if like.dtype == np.uint16 else f32
+
+
+def rms_norm(x: np.ndarray, epsilon: float = 1e-5) -> np.ndarray:
+    """Along the last axis: x / sqrt(sum(x^2)/cols + epsilon)
+    (probe-capabilities.py:320-327). Pinned in tests/test_oracle.py by the
+    constant-row closed form, scale invariance and the unit mean square."""
+    v = _widen(x)
+    denominator = np.sqrt((v * v).sum(axis=-1, keepdims=True) / v.shape[-1] + epsilon)
+    return _narrow(v / denominator, x)
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    """Along the last axis: exp(x - max) / sum(exp(x - max))
+    (probe-capabilities.py:347-354). Pinned in tests/test_oracle.py by rows
+    summing to 1, shift invariance, the uniform and two-point closed forms,
+    and no overflow at large inputs."""
+    v = _widen(x)
+    scaled = np.exp(v - v.max(axis=-1, keepdims=True))
+    return _narrow(scaled / scaled.sum(axis=-1, keepdims=True), x)
+
+
+def index_select(x: np.ndarray, axis: int, indices: np.ndarray) -> np.ndarray:
+    """Rows (axis 0) or columns (axis 1) at the given indices, zeros for an
+    index outside the axis (probe-capabilities.py:149-176). Pinned in
+    tests/test_oracle.py by identity and reversal permutations, the zero fill
+    and the axis-1 / transposed-axis-0 equivalence."""
+    x = np.asarray(x)
+    indices = np.asarray(indices, dtype=np.int64)
+    size = x.shape[axis]
+    valid = (indices >= 0) & (indices < size)
+    taken = np.take(x, np.where(valid, indices, 0), axis=axis)
+    mask = valid[:, None] if axis == 0 else valid[None, :]
+    return np.where(mask, taken, np.zeros((), dtype=x.dtype)).astype(x.dtype)

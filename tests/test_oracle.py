@@ -376,3 +376,47 @@ def test_silu_closed_forms_and_identities(rng):
     assert np.all(np.abs(O.silu(g) - exact) <= 4 * ulp + 1e-45)
     up = rng.standard_normal(4096).astype(np.float32)
     np.testing.assert_array_equal(O.silu_gate(g, up), (O.silu(g) * up).astype(np.float32))
+
+
+# ---- decode-step ops (rms_norm, softmax, index_select) ----
+
+def test_rms_norm_closed_forms(rng):
+    """A constant row c maps to c / sqrt(c^2 + eps); the result is invariant
+    to scaling the row (up to eps); its mean square is ms / (ms + eps); bf16
+    inputs are widened exactly and the result rounded once."""
+    c = np.full((2, 64), 3.0, np.float32)
+    np.testing.assert_allclose(O.rms_norm(c), 3.0 / np.sqrt(9.0 + 1e-5), rtol=1e-7)
+    x = rng.standard_normal((4, 128)).astype(np.float32)
+    np.testing.assert_allclose(O.rms_norm(x * 8, 0.0), O.rms_norm(x, 0.0), rtol=2e-7)
+    y = O.rms_norm(x).astype(np.float64)
+    ms = (x.astype(np.float64) ** 2).mean(axis=1)
+    np.testing.assert_allclose((y ** 2).mean(axis=1), ms / (ms + 1e-5), rtol=1e-6)
+    xb = O.bf16_from_f32(x)
+    assert O.rms_norm(xb).dtype == np.uint16
+    np.testing.assert_array_equal(O.rms_norm(xb), O.bf16_from_f32(O.rms_norm(O.f32_from_bf16(xb))))
+
+
+def test_softmax_closed_forms(rng):
+    """Rows sum to 1; adding a constant changes nothing; a constant row is
+    uniform; [0, ln 3] gives [1/4, 3/4]; inputs near 1000 do not overflow."""
+    x = (rng.standard_normal((5, 320)) * 3).astype(np.float32)
+    y = O.softmax(x).astype(np.float64)
+    np.testing.assert_allclose(y.sum(axis=1), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(O.softmax(x + np.float32(5.0)), O.softmax(x), rtol=1e-5, atol=1e-12)
+    np.testing.assert_allclose(O.softmax(np.zeros((1, 7), np.float32)), 1 / 7, rtol=1e-7)
+    np.testing.assert_allclose(O.softmax(np.array([[0.0, np.log(3.0)]], np.float32)), [[0.25, 0.75]], rtol=1e-7)
+    big = O.softmax(np.array([[1000.0, 1000.0, 999.0]], np.float32))
+    assert np.all(np.isfinite(big)) and abs(float(big.sum()) - 1.0) < 1e-6
+
+
+def test_index_select_permutations_and_zero_fill(rng):
+    x = rng.standard_normal((6, 5)).astype(np.float32)
+    np.testing.assert_array_equal(O.index_select(x, 0, np.arange(6)), x)
+    np.testing.assert_array_equal(O.index_select(x, 0, np.arange(5, -1, -1)), x[::-1])
+    picked = O.index_select(x, 0, np.array([2, 6, -1, 0]))
+    np.testing.assert_array_equal(picked[[0, 3]], x[[2, 0]])
+    assert not picked[[1, 2]].any()
+    cols = np.array([4, 0, 9, 1])
+    np.testing.assert_array_equal(O.index_select(x, 1, cols), O.index_select(np.ascontiguousarray(x.T), 0, cols).T)
+    xb = O.bf16_from_f32(x)
+    np.testing.assert_array_equal(O.index_select(xb, 1, cols)[:, 0], xb[:, 4])
