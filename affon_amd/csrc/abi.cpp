@@ -716,7 +716,10 @@ static int check_rows(const void* x, int32_t dtype, int64_t rows, int64_t cols, 
   if (!is_float_dtype(dtype)) return fail(AFFON_ROCM_INVALID_SHAPE, "%s requires an f32 or bf16 tensor", op);
   if (rows <= 0 || cols <= 0) return fail(AFFON_ROCM_INVALID_SHAPE, "%s requires a non-empty rank-two tensor", op);
   uint64_t count = 0;
-  if (!mul_ok(static_cast<uint64_t>(rows), static_cast<uint64_t>(cols), &count) || count > (uint64_t(1) << 40))
+  // One wave per row (four rows per workgroup) or one thread per element:
+  // the grid must stay within 2^31 workgroups.
+  if (!mul_ok(static_cast<uint64_t>(rows), static_cast<uint64_t>(cols), &count) || count > (uint64_t(1) << 40) ||
+      rows > (int64_t(1) << 32))
     return fail(AFFON_ROCM_INVALID_SHAPE, "%s size overflows", op);
   if (x == nullptr || out == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "%s buffer is null", op);
   return AFFON_ROCM_OK;
@@ -755,7 +758,7 @@ int affon_rocm_index_select(affon_rocm_session* session, const void* x, int32_t 
   if (count <= 0 || index == nullptr) return fail(AFFON_ROCM_INVALID_SHAPE, "index_select requires indices");
   uint64_t total = 0;
   if (!mul_ok(static_cast<uint64_t>(count), static_cast<uint64_t>(axis == 0 ? cols : rows), &total) ||
-      total > (uint64_t(1) << 40))
+      total > (uint64_t(1) << 38))
     return fail(AFFON_ROCM_INVALID_SHAPE, "index_select size overflows");
   if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
   hipError_t e = affon::index_select_launch(x, dtype, rows, cols, axis, index, count, out, session->stream);
