@@ -210,12 +210,14 @@ bool policy_accepts(int policy, int numerical_class) {
 }
 
 // Shape rule for AUTO among candidates that pass their guards: the prefill
-// GEMM for M >= 64, the MFMA decode kernel for 2 <= M <= 32 with bf16 input,
-// the VALU decode kernel otherwise, the generic kernel last.
+// GEMM for M >= 64 (when the policy admits its approximate class), the MFMA
+// decode kernels for M >= 2 with bf16 input (row tiles of 32 beyond 32 rows:
+// the reassociated class's path for prefill), the VALU decode kernel
+// otherwise, the generic kernel last.
 bool auto_prefers(const Candidate& c, const affon::QmmProblem& p) {
   switch (c.impl) {
     case AFFON_ROCM_IMPL_MFMA: return p.M >= 64;
-    case AFFON_ROCM_IMPL_GEMV_MFMA: return p.M >= 2 && p.M <= 32;
+    case AFFON_ROCM_IMPL_GEMV_MFMA: return p.M >= 2;
     default: return true;
   }
 }
@@ -651,7 +653,7 @@ const char* affon_rocm_quantized_matmul_capabilities(void) {
       "\"guard\":\"gfx950; bf16 input; group_size % 32 == 0; K % 64 == 0; unit inner strides; M >= 64 when auto\","
       "\"note\":\"decoded weights rounded to bf16 in LDS, bf16 MFMA, f32 accumulation\"},"
       "{\"id\":\"rocm_quantized_matmul.gemv_mfma\",\"version\":1,\"numerical_class\":\"reassociated\","
-      "\"guard\":\"gfx950; bf16 input; M <= 32; group_size a power of two >= 64; K % 256 == 0; unit inner strides\","
+      "\"guard\":\"gfx950; bf16 input; group_size a power of two >= 64; K % 256 == 0; unit inner strides; M >= 2 when auto (rows beyond 32 in row tiles)\","
       "\"note\":\"integer codes exact in bf16, per-group scale and bias applied in f32\"},"
       "{\"id\":\"rocm_quantized_matmul.gemv\",\"version\":1,\"numerical_class\":\"reassociated\","
       "\"guard\":\"gfx950; group_size % (32/bits) == 0; unit inner strides; aligned rows\","

@@ -25,7 +25,8 @@ namespace {
 
 using namespace pipeline;
 
-constexpr int kMaxRows = 32;  // activation rows per tile: up to two blocks of 16 MFMA rows
+constexpr int kMaxRows = 32;  // activation rows per tile: up to two blocks of 16 MFMA rows; more
+                              // rows run as row tiles of 32 (grid dimension y)
 constexpr int kCols = 64;     // weight columns per workgroup (4 MFMA column tiles)
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -145,6 +146,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     a.epi.kind = a.epi.bias != nullptr ? kEpiBias : kEpiNone;
   }
   const int n0 = tile * kCols;
+  const int m0 = static_cast<int>(blockIdx.y) * kMaxRows;  // this row tile's first activation row
   // K range of this wave, in whole 4-step chunks: chunks [c0, c1) of the
   // workgroup's range, itself chunks [split*C/S, (split+1)*C/S) of K.
   const int chunks = a.K / (4 * kBK);
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
 #pragma unroll
   for (int i = 0; i < kXLoads; ++i) {
     const int row = 8 * i + (lane >> 3);
-    x_src[i] = a.x + static_cast<int64_t>(min(row, a.M - 1)) * a.xs0 + 8 * ((lane & 7) ^ (row & 7) ^ ((row >> 3) & 1));
+    x_src[i] = a.x + static_cast<int64_t>(min(m0 + row, a.M - 1)) * a.xs0 + 8 * ((lane & 7) ^ (row & 7) ^ ((row >> 3) & 1));
   }
   auto issue_a = [&](int step) {
 #pragma unroll
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
 #pragma unroll
   for (int e = 0; e < kRows * kCols / kThreads; ++e) {
     const int o = e * kThreads + tid;
-    const int row = o / kCols, col = n0 + o % kCols;
+    const int row = m0 + o / kCols, col = n0 + o % kCols;
     if (row < a.M && col < a.N) {
       const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
       if (a.splits == 1)
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
 template <int BITS, typename PT>
 hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
   const int tiles = args.seg.count > 0 ? args.seg.total_tiles : (args.N + kCols - 1) / kCols;
-  const dim3 grid(tiles * args.splits);
+  const dim3 grid(tiles * args.splits, (args.M + kMaxRows - 1) / kMaxRows);
   if (args.M <= 8)
     hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 8>), grid, dim3(kThreads), 0, stream, args);
   else if (args.M <= 16)
@@ -319,7 +321,7 @@ int vrow_layout(const QmmProblem& p) {
 
 bool gemv_mfma_supports(const QmmProblem& p) {
   if (vrow_layout(p) != 0) return true;
-  if (p.x_dtype != AFFON_ROCM_BF16 || p.M > kMaxRows) return false;
+  if (p.x_dtype != AFFON_ROCM_BF16 || p.M > (int64_t(1) << 20)) return false;
   if (p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
   // Each K step inside one group, groups addressed by shift.
   if (p.K % (4 * kBK) != 0 || p.group % kBK != 0) return false;
@@ -406,11 +408,14 @@ hipError_t tiled_launch(const QmmProblem& p, const QmmProblem* group, int count,
   a.splits = 1;
   a.split_steps = 0;  // ranges are computed per workgroup from K and splits
   a.partial = nullptr;
-  // Further K ranges over workgroups while the tiles fill less than three
-  // quarters of the CUs and every wave keeps at least two chunks.
+  // Further K ranges over workgroups while the tiles (over columns and row
+  // tiles) fill less than three quarters of the CUs and every wave keeps at
+  // least two chunks.
+  const int row_tiles = static_cast<int>((p.M + kMaxRows - 1) / kMaxRows);
   int splits = 1;
   if (l.workspace != nullptr)
-    while (splits < 8 && tiles * splits < device_cus() * 3 / 4 && chunks >= 2 * kWaves * 2 * splits) splits *= 2;
+    while (splits < 8 && tiles * row_tiles * splits < device_cus() * 3 / 4 && chunks >= 2 * kWaves * 2 * splits)
+      splits *= 2;
   if (splits > 1) {
     if (auto* w = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * columns * 4))) {
       a.splits = splits;

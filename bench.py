@@ -443,6 +443,11 @@ def main() -> int:
         if want(name):
             record(name, Workload(session, name, 512, N, K, 4, 64, policy="approximate"), bound="mfma")
             extras[name]["numerical_policy"] = "approximate"
+    # The same prefill under the default policy (reassociated class: exact codes, the row-tiled MFMA kernel).
+    name = "prefill_4bit_g64_m512_n14336_k4096_backend_equivalent"
+    if want(name):
+        record(name, Workload(session, name, 512, 14336, 4096, 4, 64), bound="mfma")
+        extras[name]["numerical_policy"] = "backend_equivalent"
     # Large prefill stress: 4-bit group 32, 2048 activation rows, both weight orientations.
     for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192", 28672, 8192),
                        ("prefill_4bit_g32_m2048_n8192_k28672", 8192, 28672)):

@@ -48,7 +48,7 @@ enum {
   AFFON_ROCM_IMPL_AUTO = 0,
   AFFON_ROCM_IMPL_GENERIC = 1,   /* rocm_quantized_matmul.generic: any view, any group */
   AFFON_ROCM_IMPL_GEMV = 2,      /* rocm_quantized_matmul.gemv: VALU decode, small M */
-  AFFON_ROCM_IMPL_GEMV_MFMA = 3, /* rocm_quantized_matmul.gemv_mfma: bf16 x, M <= 32 */
+  AFFON_ROCM_IMPL_GEMV_MFMA = 3, /* rocm_quantized_matmul.gemv_mfma: bf16 x, any M (row tiles of 32) */
   AFFON_ROCM_IMPL_MFMA = 4       /* rocm_quantized_matmul.mfma: prefill GEMM, bf16 x */
 };
 

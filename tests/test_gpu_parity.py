@@ -466,6 +466,28 @@ def test_gemv_mfma_two_row_blocks_against_oracle(session, M):
     check_against_oracle(y.numpy(), x, packed, s, b, 4, 64, True)
 
 
+@pytest.mark.parametrize("M", [33, 100, 512])
+def test_row_tiled_mfma_decode_exact_and_selected(session, M, rng):
+    """Beyond 32 activation rows the LDS-tiled gemv_mfma kernel runs row tiles
+    of 32 (grid dimension y): the reassociated class's path for prefill, which
+    the default policy selects. Integer activations and codes, power-of-two
+    scales and integer biases make every sum exact, so the output must equal
+    the f64 reference exactly (partial last row tile, split K for the small N)."""
+    for bits, N, K, group in ((4, 200, 1024, 64), (8, 72, 2048, 128), (2, 130, 1024, 64)):
+        q = rng.integers(0, 1 << bits, size=(N, K))
+        x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)
+        s = 2.0 ** rng.integers(-3, 1, size=(N, K // group))
+        b = rng.integers(-2, 3, size=(N, K // group)).astype(np.float64)
+        xt = upload(session, storage(x, "bf16"), "bf16")
+        wt = upload(session, pack_codes(q, bits), "u32")
+        st, bt = upload(session, storage(s, "bf16"), "bf16"), upload(session, storage(b, "bf16"), "bf16")
+        assert A.selected_implementation(xt, wt, st, bt, bits=bits, group_size=group) == \
+            "rocm_quantized_matmul.gemv_mfma"
+        out = A.quantized_matmul(xt, wt, st, bt, bits=bits, group_size=group).numpy()
+        np.testing.assert_array_equal(out, reference_f64(x, q, s, b, group).astype(np.float32),
+                                      err_msg=f"M={M} {bits}-bit")
+
+
 def test_gemv_mfma_selected_for_decode_batches(session):
     x, packed, s, b = seeded_problem(8, 512, 1024, 4, 64, "bf16", "bf16")
     xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
