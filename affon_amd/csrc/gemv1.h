@@ -58,6 +58,10 @@ struct Args {
   float* out;
   int64_t N;
   int cpg_shift;  // log2(16-byte chunks per group)
+  // Nonzero when every kShare<BITS> consecutive chunks of a K-part lie in one
+  // group (group size >= kShare * chunk values, part % kShare == 0): the
+  // group parameters then travel in the shared layout (see the kernel).
+  int shared_params;
   int chunks;  // 16-byte chunks per row
   int part;    // chunks per K-part
   int ks;      // K-parts per row (waves per row block)
@@ -84,6 +88,24 @@ __device__ __forceinline__ T pick(const T (&a)[kMaxSegments], int seg) {
 
 template <int BITS>
 constexpr int chunk_values() { return 128 / BITS; }
+
+// Chunks per group at group size 64 (the common case): the width of the
+// lane groups that share one parameter load in the shared layout.
+template <int BITS>
+constexpr int kShare = BITS == 8 ? 4 : BITS == 4 ? 2 : 1;
+
+// Value of lane (lane & ~(S-1)) | j of each aligned group of S lanes (S = 1,
+// 2, 4), in every lane of the group: a quad-permute DPP move.
+template <int S, int j>
+__device__ __forceinline__ uint32_t lane_group_bcast(uint32_t v) {
+  if constexpr (S == 1) {
+    return v;
+  } else {
+    constexpr int lo = j, hi = S == 4 ? j : 2 + j;  // quad lanes 0-1 / 2-3 read
+    constexpr int ctrl = lo | (lo << 2) | (hi << 4) | (hi << 6);
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), ctrl, 0xf, 0xf, false));
+  }
+}
 
 // Activations of one chunk as staged in LDS: kPieces 16-byte pieces (2..16).
 // Piece j of chunk c sits in slot j at uint4 index j * stride + (c ^ swizzle
@@ -418,12 +440,24 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // Group parameters: one per (row, chunk); rows have uniform bases, lanes a
-  // 32-bit byte offset shared by all rows.
+  // Group parameters; rows have uniform bases, lanes a 32-bit byte offset
+  // shared by all rows.
+  //   Per-lane layout: load i of a lane fetches the group of its chunk i.
+  //   Shared layout (LG = kShare lanes per lane group): in load j, lane l
+  //   fetches the group of chunk c_begin + (l & ~(LG-1)) + 64 (LG j + l % LG).
+  //   Chunk i of every lane of that lane group lies in the same group when
+  //   i = LG j + l % LG, because the LG-aligned run of chunks holding the
+  //   lane group's chunks i lies inside one group. A row then needs
+  //   ceil(CPL / LG) loads of each parameter instead of CPL, and chunk i reads
+  //   its value from lane (l & ~(LG-1)) | (i % LG) of load i / LG (spread
+  //   below, once the loads have landed).
+  constexpr int LG = kShare<BITS>;  // lanes per lane group
+  const bool shared = LG > 1 && a.shared_params != 0;
   uint32_t sraw[R][CPL], braw[R][CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    const int c = c_begin + lane + 64 * i;
+    if (shared && i * LG >= CPL) break;  // uniform
+    const int c = shared ? c_begin + (lane & ~(LG - 1)) + 64 * (LG * i + (lane & (LG - 1))) : c_begin + lane + 64 * i;
     const uint32_t goff = static_cast<uint32_t>((c < c_end ? c : 0) >> a.cpg_shift) * PT::bytes;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -472,6 +506,31 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
     if (p < pieces) v = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(p) * 16u);
     stage_pieces<BITS, XT>(v, p, pieces, xs_lds, xsum_lds, stride);
+  }
+  if (shared) {
+    constexpr int kLoads = (CPL + LG - 1) / LG;
+    uint32_t sl[R][kLoads], bl[R][kLoads];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        sl[r][i] = sraw[r][i];
+        bl[r][i] = braw[r][i];
+      }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int j = i % LG;
+        sraw[r][i] = j == 0 ? lane_group_bcast<LG, 0>(sl[r][i / LG])
+                   : j == 1 ? lane_group_bcast<LG, 1>(sl[r][i / LG])
+                   : j == 2 ? lane_group_bcast<LG, 2 % LG>(sl[r][i / LG])
+                            : lane_group_bcast<LG, 3 % LG>(sl[r][i / LG]);
+        braw[r][i] = j == 0 ? lane_group_bcast<LG, 0>(bl[r][i / LG])
+                   : j == 1 ? lane_group_bcast<LG, 1>(bl[r][i / LG])
+                   : j == 2 ? lane_group_bcast<LG, 2 % LG>(bl[r][i / LG])
+                            : lane_group_bcast<LG, 3 % LG>(bl[r][i / LG]);
+      }
   }
   __syncthreads();
 

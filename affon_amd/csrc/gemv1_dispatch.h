@@ -170,6 +170,7 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
   if (best == nullptr) return hipErrorInvalidValue;
   a.ks = best_ks;
   a.part = (a.chunks + best_ks - 1) / best_ks;
+  a.shared_params = (1 << a.cpg_shift) >= kShare<BITS> && a.part % kShare<BITS> == 0;
   return best->launch(a, stream);
 }
 
