@@ -58,12 +58,8 @@ struct Args {
   float* out;
   int64_t N;
   int cpg_shift;  // log2(16-byte chunks per group)
-  // Nonzero when every kShare<BITS> consecutive chunks of a K-part lie in one
-  // group (group size >= kShare * chunk values, part % kShare == 0): the
-  // group parameters then travel in the shared layout (see the kernel).
-  int shared_params;
   int chunks;  // 16-byte chunks per row
-  int part;    // chunks per K-part
+  int part;    // chunks per K-part (a multiple of the kernel's LG)
   int ks;      // K-parts per row (waves per row block)
   Epilogue epi;
   // Grouped mode: projection i owns launch rows [first[i], first[i] + n[i])
@@ -90,7 +86,8 @@ template <int BITS>
 constexpr int chunk_values() { return 128 / BITS; }
 
 // Chunks per group at group size 64 (the common case): the width of the
-// lane groups that share one parameter load in the shared layout.
+// lane groups that share one parameter load in the shared layout, used when
+// a group spans at least that many chunks.
 template <int BITS>
 constexpr int kShare = BITS == 8 ? 4 : BITS == 4 ? 2 : 1;
 
@@ -105,6 +102,19 @@ __device__ __forceinline__ uint32_t lane_group_bcast(uint32_t v) {
     constexpr int ctrl = lo | (lo << 2) | (hi << 4) | (hi << 6);
     return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), ctrl, 0xf, 0xf, false));
   }
+}
+
+// Chunk i's group parameter, given the shared-layout loads v of one row
+// (load i / LG, lane (lane & ~(LG-1)) | (i % LG)). i is a constant after
+// unrolling, so the selects fold to one DPP move.
+template <int LG, int N>
+__device__ __forceinline__ uint32_t param_of(const uint32_t (&v)[N], int i) {
+  const uint32_t x = v[i / LG];
+  const int j = i % LG;
+  return j == 0   ? lane_group_bcast<LG, 0>(x)
+         : j == 1 ? lane_group_bcast<LG, 1 % LG>(x)
+         : j == 2 ? lane_group_bcast<LG, 2 % LG>(x)
+                  : lane_group_bcast<LG, 3 % LG>(x);
 }
 
 // Activations of one chunk as staged in LDS: kPieces 16-byte pieces (2..16).
@@ -375,7 +385,9 @@ __device__ __forceinline__ void stage_pieces(u32x4_t v, int p, int count, uint4*
   }
 }
 
-template <int BITS, typename XT, typename PT, int R, int CPL, int MODE>
+// LG: lanes per parameter-sharing lane group (1, or kShare<BITS> when every
+// group spans at least LG chunks and K-parts start on multiples of LG).
+template <int BITS, typename XT, typename PT, int R, int CPL, int MODE, int LG>
 __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   constexpr bool PAIR = MODE == kPaired;
   static_assert(!PAIR || R % 2 == 0, "paired rows");
@@ -443,21 +455,22 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   // Group parameters; rows have uniform bases, lanes a 32-bit byte offset
   // shared by all rows.
   //   Per-lane layout: load i of a lane fetches the group of its chunk i.
-  //   Shared layout (LG = kShare lanes per lane group): in load j, lane l
+  //   Shared layout (LG > 1 lanes per lane group): in load j, lane l
   //   fetches the group of chunk c_begin + (l & ~(LG-1)) + 64 (LG j + l % LG).
   //   Chunk i of every lane of that lane group lies in the same group when
   //   i = LG j + l % LG, because the LG-aligned run of chunks holding the
   //   lane group's chunks i lies inside one group. A row then needs
   //   ceil(CPL / LG) loads of each parameter instead of CPL, and chunk i reads
-  //   its value from lane (l & ~(LG-1)) | (i % LG) of load i / LG (spread
-  //   below, once the loads have landed).
-  constexpr int LG = kShare<BITS>;  // lanes per lane group
-  const bool shared = LG > 1 && a.shared_params != 0;
-  uint32_t sraw[R][CPL], braw[R][CPL];
+  //   its value from lane (l & ~(LG-1)) | (i % LG) of load i / LG, by a DPP
+  //   move where it is used. (Aligned lane groups are wholly inside or
+  //   outside the K-part, so the lane read from is active whenever the
+  //   reading lane is.)
+  static_assert(LG == 1 || LG == kShare<BITS>, "lane group width");
+  constexpr int kLoads = (CPL + LG - 1) / LG;
+  uint32_t sraw[R][kLoads], braw[R][kLoads];
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    if (shared && i * LG >= CPL) break;  // uniform
-    const int c = shared ? c_begin + (lane & ~(LG - 1)) + 64 * (LG * i + (lane & (LG - 1))) : c_begin + lane + 64 * i;
+  for (int i = 0; i < kLoads; ++i) {
+    const int c = c_begin + (lane & ~(LG - 1)) + 64 * (LG * i + (lane & (LG - 1)));
     const uint32_t goff = static_cast<uint32_t>((c < c_end ? c : 0) >> a.cpg_shift) * PT::bytes;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -507,31 +520,6 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     if (p < pieces) v = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(p) * 16u);
     stage_pieces<BITS, XT>(v, p, pieces, xs_lds, xsum_lds, stride);
   }
-  if (shared) {
-    constexpr int kLoads = (CPL + LG - 1) / LG;
-    uint32_t sl[R][kLoads], bl[R][kLoads];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int i = 0; i < kLoads; ++i) {
-        sl[r][i] = sraw[r][i];
-        bl[r][i] = braw[r][i];
-      }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int j = i % LG;
-        sraw[r][i] = j == 0 ? lane_group_bcast<LG, 0>(sl[r][i / LG])
-                   : j == 1 ? lane_group_bcast<LG, 1>(sl[r][i / LG])
-                   : j == 2 ? lane_group_bcast<LG, 2 % LG>(sl[r][i / LG])
-                            : lane_group_bcast<LG, 3 % LG>(sl[r][i / LG]);
-        braw[r][i] = j == 0 ? lane_group_bcast<LG, 0>(bl[r][i / LG])
-                   : j == 1 ? lane_group_bcast<LG, 1>(bl[r][i / LG])
-                   : j == 2 ? lane_group_bcast<LG, 2 % LG>(bl[r][i / LG])
-                            : lane_group_bcast<LG, 3 % LG>(bl[r][i / LG]);
-      }
-  }
   __syncthreads();
 
   // 3. Decode, multiply, apply group parameters per chunk.
@@ -559,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const float acc = chunk_dot<BITS, XT>(wv[r][i], xr);
-        y[r] = fmaf(param(sraw[r][i]) * inv_unit, acc, fmaf(param(braw[r][i]), xsum, y[r]));
+        y[r] = fmaf(param(param_of<LG>(sraw[r], i)) * inv_unit, acc, fmaf(param(param_of<LG>(braw[r], i)), xsum, y[r]));
       }
     }
   }
@@ -606,14 +594,14 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
 }
 
-template <int BITS, typename XT, typename PT, int R, int CPL, int MODE>
+template <int BITS, typename XT, typename PT, int R, int CPL, int MODE, int LG>
 hipError_t launch(const Args& a, hipStream_t stream) {
   constexpr int RO = MODE == kPaired ? R / 2 : R;
   const size_t lds = lds_size<BITS, XT, R>(a.chunks);
   const int64_t row_blocks = (a.N + RO - 1) / RO;
   const int64_t per_block = kWaves / a.ks;
   const unsigned blocks = static_cast<unsigned>((row_blocks + per_block - 1) / per_block);
-  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL, MODE>), dim3(blocks), dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((kernel<BITS, XT, PT, R, CPL, MODE, LG>), dim3(blocks), dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
 

@@ -40,10 +40,10 @@ size_t lds_bytes(int chunks) {
 }
 
 #define AFFON_GEMV1_VARIANT(R, CPL)                                                     \
-  {R, CPL, launch<BITS, XT, PT, R, CPL, MODE>,                                           \
-   reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL, MODE>), lds_bytes<BITS, XT, R>}
+  {R, CPL, launch<BITS, XT, PT, R, CPL, MODE, LG>,                                       \
+   reinterpret_cast<const void*>(&kernel<BITS, XT, PT, R, CPL, MODE, LG>), lds_bytes<BITS, XT, R>}
 
-template <int BITS, typename XT, typename PT, int MODE>
+template <int BITS, typename XT, typename PT, int MODE, int LG>
 const Variant* variants(int* count) {
   if constexpr (MODE == kPaired) {
     static const Variant table[] = {
@@ -139,8 +139,13 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
   a.chunks = static_cast<int>(p.K * BITS / 128);
   a.cpg_shift = 0;
   while ((int64_t(1) << a.cpg_shift) * chunk_values<BITS>() < p.group) ++a.cpg_shift;
+  // Parameter loads are shared by lane groups of kShare<BITS> lanes when a
+  // group spans that many chunks (K-parts then start on multiples of it).
+  const bool share = (1 << a.cpg_shift) >= kShare<BITS>;
+  const int lg = share ? kShare<BITS> : 1;
   int nvariants = 0;
-  const Variant* table = variants<BITS, XT, PT, MODE>(&nvariants);
+  const Variant* table =
+      share ? variants<BITS, XT, PT, MODE, kShare<BITS>>(&nvariants) : variants<BITS, XT, PT, MODE, 1>(&nvariants);
   const int cus = device_cus();
   const Variant* best = nullptr;
   int best_ks = 0;
@@ -150,7 +155,7 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
     int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
     if (ks == 3) ks = 4;
     if (ks > 4) continue;
-    const int part = (a.chunks + ks - 1) / ks;
+    const int part = ((a.chunks + ks - 1) / ks + lg - 1) / lg * lg;
     if (v.CPL > 1 && 64 * (v.CPL - 1) >= part) continue;  // a chunk slot would stay empty
     const size_t lds = v.lds(a.chunks);
     if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
@@ -169,8 +174,7 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
   }
   if (best == nullptr) return hipErrorInvalidValue;
   a.ks = best_ks;
-  a.part = (a.chunks + best_ks - 1) / best_ks;
-  a.shared_params = (1 << a.cpg_shift) >= kShare<BITS> && a.part % kShare<BITS> == 0;
+  a.part = ((a.chunks + best_ks - 1) / best_ks + lg - 1) / lg * lg;
   return best->launch(a, stream);
 }
 
