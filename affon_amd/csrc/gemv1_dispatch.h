@@ -150,26 +150,31 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
   const Variant* best = nullptr;
   int best_ks = 0;
   int64_t best_rounds = 0, best_waves = 0;
-  for (int i = 0; i < nvariants; ++i) {
-    const Variant& v = table[i];
-    int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
-    if (ks == 3) ks = 4;
-    if (ks > 4) continue;
-    const int part = ((a.chunks + ks - 1) / ks + lg - 1) / lg * lg;
-    if (v.CPL > 1 && 64 * (v.CPL - 1) >= part) continue;  // a chunk slot would stay empty
-    const size_t lds = v.lds(a.chunks);
-    if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
-    const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
-    const int rows_out = PAIR ? v.R / 2 : v.R;
-    const int64_t waves = (a.N + rows_out - 1) / rows_out * ks;
-    const int64_t rounds = (waves + capacity - 1) / capacity;
-    const bool better = best == nullptr || rounds < best_rounds ||
-                        (rounds == best_rounds && (ks < best_ks || (ks == best_ks && waves > best_waves)));
-    if (better) {
-      best = &v;
-      best_ks = ks;
-      best_rounds = rounds;
-      best_waves = waves;
+  // Variants that would leave a chunk slot of every lane empty are passed
+  // over, unless no other variant covers the row (the K-part count is 1, 2
+  // or 4, so e.g. 688 chunks run as 4 parts of 172 on 4-chunk lanes).
+  for (int pass = 0; pass < 2 && best == nullptr; ++pass) {
+    for (int i = 0; i < nvariants; ++i) {
+      const Variant& v = table[i];
+      int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
+      if (ks == 3) ks = 4;
+      if (ks > 4) continue;
+      const int part = ((a.chunks + ks - 1) / ks + lg - 1) / lg * lg;
+      if (pass == 0 && v.CPL > 1 && 64 * (v.CPL - 1) >= part) continue;  // a chunk slot would stay empty
+      const size_t lds = v.lds(a.chunks);
+      if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
+      const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
+      const int rows_out = PAIR ? v.R / 2 : v.R;
+      const int64_t waves = (a.N + rows_out - 1) / rows_out * ks;
+      const int64_t rounds = (waves + capacity - 1) / capacity;
+      const bool better = best == nullptr || rounds < best_rounds ||
+                          (rounds == best_rounds && (ks < best_ks || (ks == best_ks && waves > best_waves)));
+      if (better) {
+        best = &v;
+        best_ks = ks;
+        best_rounds = rounds;
+        best_waves = waves;
+      }
     }
   }
   if (best == nullptr) return hipErrorInvalidValue;

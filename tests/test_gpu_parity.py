@@ -304,6 +304,32 @@ def test_decode_integer_products_exact(session, bits, x_dtype, p_dtype, rng):
             np.testing.assert_array_equal(out, expected.astype(np.float32), err_msg=f"{impl} {M}x{N}x{K} g{group}")
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_decode_m1_parameter_layouts_exact(session, bits, group, rng):
+    """The M=1 kernel loads group parameters once per lane group when a group
+    spans at least 2 (4-bit) or 4 (8-bit) 16-byte chunks (g64, g128), and per
+    lane otherwise (g32), with K-parts rounded up to the lane-group width
+    (8-bit K=4160: 260 chunks in parts of 132 and 128). Integer data make the
+    products exact."""
+    for N, K in [(67, 4160), (40, 11008), (13, 4096)]:
+        if K % group:
+            continue
+        q = rng.integers(0, 1 << bits, size=(N, K))
+        x = rng.integers(-3, 4, size=(1, K)).astype(np.float64)
+        s = 2.0 ** rng.integers(-2, 2, size=(N, K // group))
+        b = rng.integers(-2, 3, size=(N, K // group)).astype(np.float64)
+        expected = reference_f64(x, q, s, b, group).astype(np.float32)
+        xt = upload(session, storage(x, "bf16"), "bf16")
+        wt = upload(session, pack_codes(q, bits), "u32")
+        st, bt = upload(session, storage(s, "bf16"), "bf16"), upload(session, storage(b, "bf16"), "bf16")
+        assert A.selected_implementation(xt, wt, st, bt, bits=bits, group_size=group,
+                                         implementation="gemv") == "rocm_quantized_matmul.gemv"
+        out = session.empty("f32", (1, N))
+        A.quantized_matmul_into(out, xt, wt, st, bt, bits=bits, group_size=group, implementation="gemv")
+        np.testing.assert_array_equal(out.numpy(), expected, err_msg=f"{bits}-bit g{group} {N}x{K}")
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_decode_sweep_full_size(session, M):
     """8-bit group-64 decode sweep at 14336x4096, bf16 operands, full output."""
