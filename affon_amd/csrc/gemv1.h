@@ -18,6 +18,11 @@
 //     v_cvt_f32_ubyte for 8-bit codes) and multiplied with v_dot2_f32_bf16
 //     (bf16 x) or v_fma_f32 (f32 x); each chunk lies inside one group, so its
 //     parameters are applied once per chunk: y += s * sum(x*q) + b * sum(x);
+//   * when a group spans LG > 1 chunks (8-bit and 4-bit codes at group size
+//     64 and up), aligned groups of LG lanes load the parameters of LG
+//     different groups at once and each chunk takes its value from its lane
+//     group with a quad-permute DPP move: ceil(CPL / LG) loads per row and
+//     parameter instead of CPL, and fewer live registers;
 //   * rows are reduced across the wave with butterfly shuffles and across the
 //     K-parts of a workgroup through LDS;
 //   * in paired mode the wave's first R/2 rows are rows of a gate projection
