@@ -33,6 +33,8 @@ pytestmark = pytest.mark.gpu
 CASES = [
     (1, 300, 512, 4, 64, "bf16", "bf16"),
     (1, 96, 4096, 8, 64, "f32", "f32"),
+    (1, 200, 1024, 8, 32, "bf16", "bf16"),  # M=1 kernel, parameters loaded per lane (groups of 2 chunks)
+    (1, 136, 2048, 4, 32, "bf16", "bf16"),  # M=1 kernel, one chunk per group
     (2, 136, 1024, 8, 64, "bf16", "bf16"),
     (4, 72, 512, 4, 32, "bf16", "f32"),
     (16, 128, 1024, 4, 64, "bf16", "bf16"),
@@ -202,19 +204,22 @@ def test_epilogue_validation_leaves_output_untouched(session):
     np.testing.assert_array_equal(out.numpy(), np.full((1, 64), 7.0, np.float32))
 
 
-@pytest.mark.parametrize("x_dtype,p_dtype,bits", [("bf16", "bf16", 4), ("f32", "f32", 8), ("bf16", "f32", 2)])
+@pytest.mark.parametrize("x_dtype,p_dtype,bits,group", [("bf16", "bf16", 4, 64), ("f32", "f32", 8, 64),
+                                                        ("bf16", "f32", 2, 64), ("bf16", "bf16", 4, 32),
+                                                        ("bf16", "bf16", 8, 32)])
 @pytest.mark.parametrize("sizes", [(4096, 1024, 1024), (300, 77, 13, 8)], ids=["qkv", "ragged"])
-def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, sizes, rng):
+def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, group, sizes, rng):
     """Projections of one input in one launch (M = 1: the gemv kernel; M = 16
     with bf16 activations: the LDS-tiled gemv_mfma kernel, whose split-K
     partials span all projections) or in sequence (M = 2), with output biases
-    on some of them; ragged sizes exercise the padding between projections."""
+    on some of them; ragged sizes exercise the padding between projections.
+    Group 32 at 4 and 8 bits takes the M=1 kernel's per-lane parameter loads."""
     K = 1024
     for M in (1, 2, 16):
         projections, host = [], []
-        x = seeded_problem(M, 8, K, bits, 64, x_dtype, p_dtype, seed=59)[0]
+        x = seeded_problem(M, 8, K, bits, group, x_dtype, p_dtype, seed=59)[0]
         for i, n in enumerate(sizes):
-            _, packed, s, b = seeded_problem(M, n, K, bits, 64, x_dtype, p_dtype, seed=60 + 2 * i)
+            _, packed, s, b = seeded_problem(M, n, K, bits, group, x_dtype, p_dtype, seed=60 + 2 * i)
             parts = [upload(session, a, dtype_of(a)) for a in (packed, s, b)]
             bias = None
             if i % 2 == 0:
@@ -223,17 +228,17 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, siz
             projections.append(tuple(parts))
             host.append((packed, s, b, bias))
         xt = upload(session, x, dtype_of(x))
-        plan = A.grouped_plan(xt, projections, bits=bits, group_size=64)
-        one_launch = M == 1 or (M == 16 and x_dtype == "bf16")
+        plan = A.grouped_plan(xt, projections, bits=bits, group_size=group)
+        one_launch = M == 1 or (M == 16 and x_dtype == "bf16" and group % 64 == 0)  # tiled: K steps of 64
         if one_launch:
             kernel = "gemv" if M == 1 else "gemv_mfma"
             assert plan == f"rocm_quantized_matmul.{kernel}[grouped:{len(sizes)},bias]", plan
         else:
             assert plan.count(";") == len(sizes) - 1, plan
-        outs = A.quantized_matmul_grouped(xt, projections, bits=bits, group_size=64)
+        outs = A.quantized_matmul_grouped(xt, projections, bits=bits, group_size=group)
         for out, (packed, s, b, bias), parts in zip(outs, host, projections):
-            expected = O.quantized_matmul(x, packed, s, b, bits, 64)
-            single = A.quantized_matmul(xt, *parts[:3], bits=bits, group_size=64).numpy()
+            expected = O.quantized_matmul(x, packed, s, b, bits, group)
+            single = A.quantized_matmul(xt, *parts[:3], bits=bits, group_size=group).numpy()
             if bias is not None:
                 expected = O.add_output_bias(expected, bias)
                 single = O.add_output_bias(single, bias)
