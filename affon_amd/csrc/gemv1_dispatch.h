@@ -1,16 +1,24 @@
 // Host-side shape selection for the M = 1 decode kernel.
 //
 // For every (R rows, CPL chunks per lane) variant the number of K-parts is the
-// smallest that gives each lane at most CPL chunks; the variant chosen is the
-// one that runs in the fewest rounds of resident waves (occupancy from the
-// compiled kernel), then with the fewest K-parts (no LDS reduction and
-// barrier), then with the most waves (more latency hiding). On MI355X this
-// picks the fastest variant, or one within 3% of it, on each of 8-bit
-// 14336x4096 and 4096x14336, 4-bit 14336x4096, 4096x14336, 4096x4096,
-// 1024x4096 and 128256x4096 (bf16), and 4-bit 4096x4096 with f32 operands.
-// Paired gate/up problems choose among the even-R variants the same way,
-// counting R/2 output rows per wave; grouped launches count the rows of all
-// their projections (each padded to a multiple of 8).
+// smallest that gives each lane at most CPL chunks (1, 2 or 4 parts). The
+// choice, in order of precedence:
+//   * no lane slot left empty by every K-part, and at least XT bytes * 8 /
+//     BITS weight rows per workgroup (each workgroup stages the whole
+//     activation row from L2; fewer rows make that staging outweigh the
+//     packed words);
+//   * the least work on the busiest SIMD -- waves per SIMD, rounded up, times
+//     the chunk-rows of a wave -- within 5 % (an uneven last wave per SIMD is
+//     a tail the whole launch waits for);
+//   * the fewest rounds of resident waves (occupancy from the compiled
+//     kernel), then the fewest K-parts, then the most waves.
+// On MI355X (graph periods, random data) this picks the fastest variant, or
+// one within 1 % of it, on each of 8-bit 14336x4096 and 4096x14336, 4-bit
+// 14336x4096, 4096x14336, 4096x4096, 1024x4096 and 128256x4096 (bf16), and
+// 4-bit 4096x4096 with f32 operands. Paired gate/up problems choose among the
+// even-R variants the same way, counting R/2 output rows per wave; grouped
+// launches count the rows of all their projections (each padded to a
+// multiple of 8).
 #pragma once
 
 #include <map>
@@ -146,37 +154,62 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
   int nvariants = 0;
   const Variant* table =
       share ? variants<BITS, XT, PT, MODE, kShare<BITS>>(&nvariants) : variants<BITS, XT, PT, MODE, 1>(&nvariants);
+  // Candidates, each with the measures the choice uses.
+  struct Candidate {
+    const Variant* v;
+    int ks, tier;
+    int64_t waves, rounds, load;
+  };
+  Candidate cand[16];
+  int ncand = 0;
   const int cus = device_cus();
-  const Variant* best = nullptr;
-  int best_ks = 0;
-  int64_t best_rounds = 0, best_waves = 0;
-  // Variants that would leave a chunk slot of every lane empty are passed
-  // over, unless no other variant covers the row (the K-part count is 1, 2
-  // or 4, so e.g. 688 chunks run as 4 parts of 172 on 4-chunk lanes).
-  for (int pass = 0; pass < 2 && best == nullptr; ++pass) {
-    for (int i = 0; i < nvariants; ++i) {
-      const Variant& v = table[i];
-      int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
-      if (ks == 3) ks = 4;
-      if (ks > 4) continue;
-      const int part = ((a.chunks + ks - 1) / ks + lg - 1) / lg * lg;
-      if (pass == 0 && v.CPL > 1 && 64 * (v.CPL - 1) >= part) continue;  // a chunk slot would stay empty
-      const size_t lds = v.lds(a.chunks);
-      if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
-      const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
-      const int rows_out = PAIR ? v.R / 2 : v.R;
-      const int64_t waves = (a.N + rows_out - 1) / rows_out * ks;
-      const int64_t rounds = (waves + capacity - 1) / capacity;
-      const bool better = best == nullptr || rounds < best_rounds ||
-                          (rounds == best_rounds && (ks < best_ks || (ks == best_ks && waves > best_waves)));
-      if (better) {
-        best = &v;
-        best_ks = ks;
-        best_rounds = rounds;
-        best_waves = waves;
-      }
-    }
+  const int64_t simds = static_cast<int64_t>(cus) * 4;
+  // Weight rows per workgroup that keep the activation staging (K * x bytes
+  // per workgroup, from L2) at most the packed bytes of those rows.
+  const int min_rows = XT::bytes * 8 / BITS;
+  for (int i = 0; i < nvariants && ncand < 16; ++i) {
+    const Variant& v = table[i];
+    int ks = static_cast<int>((a.chunks + 64 * v.CPL - 1) / (64 * v.CPL));
+    if (ks == 3) ks = 4;
+    if (ks > 4) continue;
+    const int part = ((a.chunks + ks - 1) / ks + lg - 1) / lg * lg;
+    const size_t lds = v.lds(a.chunks);
+    if (lds > static_cast<size_t>(kMaxLdsBytes)) continue;
+    const bool empty_slot = v.CPL > 1 && 64 * (v.CPL - 1) >= part;
+    const bool thin = kWaves * v.R / ks < min_rows;
+    Candidate c;
+    c.v = &v;
+    c.ks = ks;
+    c.tier = empty_slot ? 2 : thin ? 1 : 0;
+    const int rows_out = PAIR ? v.R / 2 : v.R;
+    c.waves = (a.N + rows_out - 1) / rows_out * ks;
+    const int64_t capacity = static_cast<int64_t>(blocks_per_cu(v.fn, lds)) * cus * kWaves;
+    c.rounds = (c.waves + capacity - 1) / capacity;
+    // Chunk-rows on the busiest SIMD: waves per SIMD (rounded up) times the
+    // chunk-rows of one wave.
+    c.load = (c.waves + simds - 1) / simds * v.R * ((part + 63) / 64);
+    cand[ncand++] = c;
   }
+  // The lowest tier present (no empty lane slot and enough rows per
+  // workgroup; then the thin ones; then those with an empty slot). Within
+  // it, variants whose busiest-SIMD load is within 5 % of the least; among
+  // those the fewest rounds of resident waves, then the fewest K-parts, then
+  // the most waves.
+  int tier = 3;
+  for (int i = 0; i < ncand; ++i) tier = cand[i].tier < tier ? cand[i].tier : tier;
+  int64_t least = -1;
+  for (int i = 0; i < ncand; ++i)
+    if (cand[i].tier == tier && (least < 0 || cand[i].load < least)) least = cand[i].load;
+  const Candidate* pick = nullptr;
+  for (int i = 0; i < ncand; ++i) {
+    const Candidate& c = cand[i];
+    if (c.tier != tier || c.load * 100 > least * 105) continue;
+    const bool better = pick == nullptr || c.rounds < pick->rounds ||
+                        (c.rounds == pick->rounds && (c.ks < pick->ks || (c.ks == pick->ks && c.waves > pick->waves)));
+    if (better) pick = &c;
+  }
+  const Variant* best = pick != nullptr ? pick->v : nullptr;
+  const int best_ks = pick != nullptr ? pick->ks : 0;
   if (best == nullptr) return hipErrorInvalidValue;
   a.ks = best_ks;
   a.part = ((a.chunks + best_ks - 1) / best_ks + lg - 1) / lg * lg;
