@@ -65,7 +65,8 @@ struct Args {
   int cpg_shift;  // log2(16-byte chunks per group)
   int chunks;  // 16-byte chunks per row
   int part;    // chunks per K-part (a multiple of the kernel's LG)
-  int ks;      // K-parts per row (waves per row block)
+  int ks;      // K-parts per row (waves per row block): 1, 2 or 4
+  int ks_shift;  // log2(ks)
   Epilogue epi;
   // Grouped mode: projection i owns launch rows [first[i], first[i] + n[i])
   // (first[0] = 0, each first a multiple of 8), with the strides above.
@@ -409,8 +410,8 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   // row addressing on the scalar unit.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int kp = wave % a.ks;
-  int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves / a.ks) + wave / a.ks) * RO;
+  const int kp = wave & (a.ks - 1);
+  int64_t n0 = (static_cast<int64_t>(blockIdx.x) * (kWaves >> a.ks_shift) + (wave >> a.ks_shift)) * RO;
   const int c_begin = kp * a.part;
   const int c_end = min(a.chunks, c_begin + a.part);
   // The wave's projection: the launch's, or in grouped mode the one whose
@@ -449,11 +450,15 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   constexpr int kEarly = 8;  // pieces per thread loaded before the packed words
   const int pieces = a.chunks * XS::kPieces;
   const int wave_piece = wave * 64;
+  // A round of pieces is loaded when any of it exists (a uniform test, so
+  // absent rounds cost no vector instructions); lanes past the row read its
+  // last piece, which staging ignores.
   u32x4_t xp[kEarly];
 #pragma unroll
   for (int e = 0; e < kEarly; ++e) {
-    const int p = wave_piece + e * kThreads + lane;
-    if (p < pieces) xp[e] = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(p) * 16u);
+    const int base = wave_piece + e * kThreads;
+    if (base < pieces)
+      xp[e] = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(min(base + lane, pieces - 1)) * 16u);
   }
   __builtin_amdgcn_sched_barrier(0);
 

@@ -212,6 +212,7 @@ hipError_t dispatch(const QmmProblem& p, const QmmProblem* group, int count, hip
   const int best_ks = pick != nullptr ? pick->ks : 0;
   if (best == nullptr) return hipErrorInvalidValue;
   a.ks = best_ks;
+  a.ks_shift = best_ks == 1 ? 0 : best_ks == 2 ? 1 : 2;
   a.part = ((a.chunks + best_ks - 1) / best_ks + lg - 1) / lg * lg;
   return best->launch(a, stream);
 }
