@@ -454,11 +454,16 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   // absent rounds cost no vector instructions); lanes past the row read its
   // last piece, which staging ignores.
   u32x4_t xp[kEarly];
-#pragma unroll
-  for (int e = 0; e < kEarly; ++e) {
+  auto load_round = [&](int e) {
     const int base = wave_piece + e * kThreads;
     if (base < pieces)
       xp[e] = *reinterpret_cast<const u32x4_t*>(a.x + static_cast<uint32_t>(min(base + lane, pieces - 1)) * 16u);
+  };
+  load_round(0);
+  load_round(1);
+  if (wave_piece + 2 * kThreads < pieces) {  // rows of more than two rounds (one uniform test for the rest)
+#pragma unroll
+    for (int e = 2; e < kEarly; ++e) load_round(e);
   }
   __builtin_amdgcn_sched_barrier(0);
 

@@ -13,7 +13,7 @@
 //   * the fewest rounds of resident waves (occupancy from the compiled
 //     kernel), then the fewest K-parts, then the most waves.
 // On MI355X (graph periods, random data) this picks the fastest variant, or
-// one within 1 % of it, on each of 8-bit 14336x4096 and 4096x14336, 4-bit
+// one within 2 % of it, on each of 8-bit 14336x4096 and 4096x14336, 4-bit
 // 14336x4096, 4096x14336, 4096x4096, 1024x4096 and 128256x4096 (bf16), and
 // 4-bit 4096x4096 with f32 operands. Paired gate/up problems choose among the
 // even-R variants the same way, counting R/2 output rows per wave; grouped
