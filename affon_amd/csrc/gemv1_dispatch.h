@@ -13,9 +13,10 @@
 //   * the fewest rounds of resident waves (occupancy from the compiled
 //     kernel), then the fewest K-parts, then the most waves.
 // On MI355X (graph periods, random data) this picks the fastest variant, or
-// one within 2 % of it, on each of 8-bit 14336x4096 and 4096x14336, 4-bit
-// 14336x4096, 4096x14336, 4096x4096, 1024x4096 and 128256x4096 (bf16), and
-// 4-bit 4096x4096 with f32 operands. Paired gate/up problems choose among the
+// one within 2 % of it, on each of 8-bit 14336x4096, 4096x14336, 4096x4096
+// and 1024x4096, 4-bit 14336x4096, 4096x14336, 11008x4096, 4096x11008,
+// 4096x4096, 2048x2048, 1024x4096 and 128256x4096, 2-bit 14336x4096 (bf16),
+// and 4-bit 4096x4096 with f32 operands. Paired gate/up problems choose among the
 // even-R variants the same way, counting R/2 output rows per wave; grouped
 // launches count the rows of all their projections (each padded to a
 // multiple of 8).
