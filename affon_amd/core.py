@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import ctypes
 import itertools
+import weakref
 from dataclasses import dataclass
 from typing import Any, Callable, Mapping, Sequence
 
@@ -67,7 +68,9 @@ def host_storage(values: Any, dtype: str) -> np.ndarray:
 
 
 class _Buffer:
-    """One device allocation; freed when the last tensor using it is gone."""
+    """One device allocation; freed when the last tensor using it is gone, or
+    by the native session when the Session is disposed first (the session
+    frees every allocation it still owns)."""
 
     def __init__(self, session: "Session", nbytes: int):
         self.session = session
@@ -75,6 +78,7 @@ class _Buffer:
         ptr = ctypes.c_void_p()
         _native.check(_native.load().affon_rocm_alloc(session._handle, max(nbytes, 1), ctypes.byref(ptr)), "alloc")
         self.ptr = ptr.value
+        session._buffers.add(self)
 
     def release(self) -> None:
         if self.ptr is not None and self.session._handle is not None:
@@ -197,6 +201,7 @@ class Session:
         self.device = device
         self._handle = handle.value
         self._executables: dict[tuple, "Executable"] = {}
+        self._buffers: "weakref.WeakSet[_Buffer]" = weakref.WeakSet()
 
     @property
     def stream(self) -> int:
@@ -263,9 +268,14 @@ class Session:
         return executable
 
     def dispose(self) -> None:
+        """Ends the session. Device memory of tensors still alive is freed
+        with it; those tensors then report that they have been disposed."""
         if self._handle is not None:
             _native.load().affon_rocm_session_destroy(self._handle)
             self._handle = None
+            for buffer in list(self._buffers):
+                buffer.ptr = None
+            self._buffers = weakref.WeakSet()
 
     def __enter__(self) -> "Session":
         return self

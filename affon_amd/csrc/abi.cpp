@@ -14,6 +14,7 @@
 #include <limits>
 #include <mutex>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "affon_rocm.h"
@@ -23,24 +24,34 @@ struct affon_rocm_session {
   int device = 0;
   hipStream_t stream = nullptr;
   affon::Workspace* workspace = nullptr;
+  // Allocations made through affon_rocm_alloc and not yet freed: the
+  // session frees them when it ends, so tensors that outlive it leak nothing.
+  std::unordered_set<void*> allocations;
 };
 
 namespace affon {
 
 Workspace::~Workspace() {
-  if (ptr_ != nullptr && hipSetDevice(device_) == hipSuccess) (void)hipFree(ptr_);
+  if (hipSetDevice(device_) != hipSuccess) return;
+  if (ptr_ != nullptr) (void)hipFree(ptr_);
+  for (void* p : retired_) (void)hipFree(p);
 }
 
 void* Workspace::get(size_t bytes) {
   if (bytes <= bytes_) return ptr_;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream_, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) return nullptr;
-  // Work already enqueued may still use the old memory.
-  if (hipStreamSynchronize(stream_) != hipSuccess) return nullptr;
-  if (ptr_ != nullptr) (void)hipFree(ptr_);
+  // The old buffer stays allocated (retired) until the session ends: work
+  // already enqueued, and graphs captured with its address, may still use it.
+  if (ptr_ != nullptr) {
+    retired_.push_back(ptr_);
+    retired_bytes_ = bytes_;
+  }
   ptr_ = nullptr;
   bytes_ = 0;
-  const size_t rounded = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+  // Grow at least twofold, so that retired buffers stay few.
+  const size_t want = bytes > 2 * retired_bytes_ ? bytes : 2 * retired_bytes_;
+  const size_t rounded = (want + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
   if (hipMalloc(&ptr_, rounded) != hipSuccess) {
     ptr_ = nullptr;
     (void)hipGetLastError();
@@ -297,6 +308,7 @@ int affon_rocm_session_destroy(affon_rocm_session* session) {
   if (hipSetDevice(session->device) == hipSuccess && session->stream != nullptr) {
     hipError_t e = hipStreamSynchronize(session->stream);
     if (e != hipSuccess) status = hip_fail(e, "hipStreamSynchronize");
+    for (void* ptr : session->allocations) (void)hipFree(ptr);
     delete session->workspace;
     e = hipStreamDestroy(session->stream);
     if (e != hipSuccess && status == AFFON_ROCM_OK) status = hip_fail(e, "hipStreamDestroy");
@@ -319,6 +331,7 @@ int affon_rocm_alloc(affon_rocm_session* session, size_t bytes, void** out) {
   *out = nullptr;
   hipError_t e = hipMalloc(out, bytes == 0 ? 1 : bytes);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  session->allocations.insert(*out);
   return AFFON_ROCM_OK;
 }
 
@@ -327,6 +340,8 @@ int affon_rocm_free(affon_rocm_session* session, void* ptr) {
   int status = check_session(session);
   if (status != AFFON_ROCM_OK) return status;
   if (ptr == nullptr) return AFFON_ROCM_OK;
+  if (session->allocations.erase(ptr) == 0)
+    return fail(AFFON_ROCM_CORE_FAILURE, "free of memory this session did not allocate");
   hipError_t e = hipStreamSynchronize(session->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   e = hipFree(ptr);
@@ -732,8 +747,9 @@ int affon_rocm_rms_norm(affon_rocm_session* session, const void* x, int32_t dtyp
   clear_error();
   int status = check_rows(x, dtype, rows, cols, out, "rms_norm");
   if (status != AFFON_ROCM_OK) return status;
-  if (!(epsilon >= 0.0f) || epsilon == std::numeric_limits<float>::infinity())
-    return fail(AFFON_ROCM_INVALID_SHAPE, "rms_norm epsilon must be finite and non-negative");
+  // program.ts:578-579: a finite, positive epsilon.
+  if (!(epsilon > 0.0f) || epsilon == std::numeric_limits<float>::infinity())
+    return fail(AFFON_ROCM_INVALID_SHAPE, "invalid rms_norm options: epsilon must be finite and positive");
   if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
   hipError_t e = affon::rms_norm_launch(x, dtype, rows, cols, epsilon, out, session->stream);
   if (e != hipSuccess) return hip_fail(e, "rms_norm");

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <vector>
 
 #include "affon_rocm.h"
 #include "epilogue.h"
@@ -30,6 +31,9 @@ struct QmmProblem {
 };
 
 // Device scratch memory owned by a session and ordered by its stream.
+// Buffers it outgrows are retired, not freed, until the session ends: a
+// graph captured earlier keeps the old address in its kernel arguments and
+// may still be replayed.
 class Workspace {
  public:
   Workspace(int device, hipStream_t stream) : device_(device), stream_(stream) {}
@@ -39,12 +43,15 @@ class Workspace {
   // At least `bytes` of device memory, or nullptr when it cannot grow now
   // (the stream is being captured into a graph, or the allocation failed).
   void* get(size_t bytes);
+  size_t retired() const { return retired_.size(); }
 
  private:
   int device_;
   hipStream_t stream_;
   void* ptr_ = nullptr;
   size_t bytes_ = 0;
+  std::vector<void*> retired_;
+  size_t retired_bytes_ = 0;  // size of the last retired buffer
 };
 
 // Where a launcher enqueues its work.

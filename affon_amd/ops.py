@@ -535,8 +535,8 @@ def rms_norm(x: Any, axis: int, epsilon: float = 1e-5) -> Any:
     """x / sqrt(mean(x^2 along axis) + epsilon), computed in f32."""
     _last_axis("rms_norm", x, axis)
     epsilon = float(epsilon)
-    if not np.isfinite(epsilon) or epsilon < 0:
-        raise TypeError("rms_norm epsilon must be finite and non-negative")
+    if not np.isfinite(epsilon) or epsilon <= 0:  # program.ts:578-579
+        raise TypeError("invalid rms_norm options: epsilon must be finite and positive")
     if isinstance(x, FormalTensor):
         return x.builder.emit("rms_norm", (x,), x.spec, {"axis": axis, "epsilon": epsilon})
     if not isinstance(x, Tensor):

@@ -2,16 +2,21 @@
 """Benchmark of the rocm weight-quantized linear path on one MI355X.
 
 A step is one quantized_matmul launch over one batch of synthetic input with
-the inputs already resident in HBM. The reported workload is the decode batch
-GEMV at 8-bit group 64: W [14336, 4096] packed u32 with bf16 scales/biases,
-x bf16 [1, 4096] from Affon's seeded generator (x: seed 1 N(0,1); W: seed 2
-N(0,0.02), quantized on the GPU). The same run also measures the 8-bit M sweep
-{2,4,8,16}, the 4-bit group-64 headline GEMV at 14336x4096, the f32 4096x4096
-4-bit case and (when available) the M=512 prefill, each as an extra field.
+the inputs already resident in HBM. The reported workload (`value`,
+`roofline`) is the 4-bit group-64 decode GEMV: W [14336, 4096] packed u32
+(8 codes per word) with bf16 scales/biases, x bf16 [1, 4096], f32 out, from
+Affon's seeded generator (x: seed 1 N(0,1); W: seed 2 N(0,0.02), quantized on
+the GPU). `roofline_prefill` is the M=512 prefill of the same weight format
+(x bf16 [512, 4096], W [14336, 4096]) against the bf16 MFMA peak. The same run
+measures, as extra fields, the 8-bit decode sweep M in {1,2,4,8,16}, 4-bit
+M=16, both prefill orientations (approximate and default policies), the
+2048-row group-32 stress shapes, the Llama-8B-shaped layer sequences at M=1
+and M=32, and the f32 4096x4096 4-bit case.
 
 Timing: the K timed steps are captured once into a HIP graph on the session's
-stream and replayed; HIP events recorded on that stream bracket the replay, so
-the per-step time is the GPU's back-to-back launch period without host
+stream; after an untimed replay, the graph is replayed REPLAYS times, each
+bracketed by HIP events recorded on that stream, and the median replay gives
+the per-step time: the GPU's back-to-back launch period without host
 overhead. Weight sets are rotated (>= 9 sets, > 600 MB in total) so that the
 256 MB Infinity Cache cannot hold the working set.
 
@@ -38,6 +43,7 @@ METRIC = "quant matmul GB/s (M=1) & TFLOP/s (M=512); % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 ROTATION_BYTES = 600e6
+REPLAYS = 5
 
 
 class Hip:
@@ -114,12 +120,14 @@ class Workload:
             raise RuntimeError(_native.last_error())
 
     def time(self, hip: Hip, steps: int, warmup: int, use_graph: bool = True) -> float:
-        """Returns milliseconds per step over `steps` back-to-back launches."""
+        """Milliseconds per step: the median over REPLAYS timed runs of `steps`
+        back-to-back launches (graph replays, or direct launches with
+        --launch stream). Every run's figure is kept in self.replay_ms."""
         stream = ctypes.c_void_p(self.session.stream)
         for i in range(warmup):
             self.launch(i)
         self.session.synchronize()
-        start, stop = hip.event(), hip.event()
+        exe = graph = None
         if use_graph:
             graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
             hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed
@@ -129,24 +137,28 @@ class Workload:
             hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
             hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")  # untimed replay
             self.session.synchronize()
+        start, stop = hip.event(), hip.event()
+        runs = []
+        for _ in range(REPLAYS):
             hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-            hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+            if use_graph:
+                hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+            else:
+                for i in range(steps):
+                    self.launch(i)
             hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
-        else:
-            hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-            for i in range(steps):
-                self.launch(i)
-            hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
-        hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+            hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+            ms = ctypes.c_float()
+            hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+            runs.append(ms.value / steps)
         self.session.synchronize()
-        ms = ctypes.c_float()
-        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
         if use_graph:
             hip.lib.hipGraphExecDestroy(exe)
             hip.lib.hipGraphDestroy(graph)
         hip.lib.hipEventDestroy(start)
         hip.lib.hipEventDestroy(stop)
-        return ms.value / steps
+        self.replay_ms = runs
+        return sorted(runs)[len(runs) // 2]
 
     def host_operands(self):
         packed, scales, biases = self.weights[0]
@@ -157,74 +169,78 @@ class Workload:
         self.descs.clear()
 
 
-def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0) -> dict:
-    """The oracle (the restated scalar CPU kernel) timed on this host, single
-    threaded as the reference's CPU kernel is (AFFON_CPU_THREADS=1), over a
-    bounded sample of about `seconds` of CPU work: a prefix of output rows
-    when the whole workload takes longer, else repeated whole passes. Also
-    checks the rows it computed against the GPU output."""
-    from oracle import oracle as O
-    x, packed, scales, biases = work.host_operands()
-    M, N, K = work.M, work.N, work.K
-    probe = min(N, 64)
-    t0 = time.perf_counter()
-    O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, probe))
-    per_row = (time.perf_counter() - t0) / probe
-    rows = int(min(N, max(probe, seconds / max(per_row, 1e-9))))
-    passes = max(1, int(seconds / max(per_row * N, 1e-9))) if rows == N else 1
-    t0 = time.perf_counter()
-    for _ in range(passes):
-        ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, rows))
-    elapsed = time.perf_counter() - t0
-    xbytes = 2 if work.x_dtype == "bf16" else 4
-    pbytes = 2 if work.p_dtype == "bf16" else 4
-    sample_bytes = passes * algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
-    err = float(np.abs(gpu_out[:, :rows].astype(np.float64) - ref[:, :rows]).max())
+def _cpu_name() -> str:
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
             cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
     except (OSError, StopIteration):
         pass
-    return {"value": round(sample_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle scalar quantized_matmul over the timed workload, "
-                       + (f"{passes} whole passes" if rows == N else f"rows 0..{rows} of {N} ({rows / N:.1%})")
-                       + f", {elapsed:.1f} s on 1 thread; host {cpu}, nproc {os.cpu_count()}"),
-            "max_abs_err_vs_gpu": err}
+    return cpu
 
 
-def cpu_baseline_parallel(work: Workload, gpu_out: np.ndarray, seconds: float = 5.0) -> dict:
-    """The same oracle loop split over output columns on the host's cores
-    (threads; the C call releases the interpreter lock), repeated whole
-    passes for about `seconds`: the multi-core CPU figure beside the
-    single-threaded one. Checks its output against the GPU's."""
+def _host_cores() -> int:
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(16, cores))  # the GPU box's CPU share is 16 cores
+
+
+def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, threads: int = 1) -> dict:
+    """The reference's scalar CPU kernel as restated in oracle/cpu_baseline.c
+    (one specialised loop per bit width and dtype pair, ordered f32, decode
+    inside the dot product), timed on this host over a bounded sample of
+    about `seconds`: repeated whole passes of the workload, or a prefix of
+    output rows when one pass takes longer. With threads > 1 the output rows
+    are split over that many threads (the C call releases the interpreter
+    lock). Checks its output against the GPU's and the oracle's."""
     from concurrent.futures import ThreadPoolExecutor
     from oracle import oracle as O
     x, packed, scales, biases = work.host_operands()
-    M, N = work.M, work.N
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    threads = max(1, min(16, cores, N))
-    bounds = [(N * i // threads, N * (i + 1) // threads) for i in range(threads)]
+    M, N, K = work.M, work.N, work.K
     out = np.zeros((M, N), dtype=np.float32)
 
-    def one_pass(pool):
-        list(pool.map(lambda r: O.quantized_matmul(x, packed, scales, biases, work.bits, work.group,
-                                                   n_range=r, out=out), bounds))
+    def run(rows, pool):
+        bounds = [(rows * i // threads, rows * (i + 1) // threads) for i in range(threads)]
+        call = lambda r: O.baseline_quantized_matmul(x, packed, scales, biases, work.bits, work.group,
+                                                     n_range=r, out=out)
+        if pool is None:
+            call((0, rows))
+        else:
+            list(pool.map(call, bounds))
 
-    with ThreadPoolExecutor(threads) as pool:
+    with ThreadPoolExecutor(threads) if threads > 1 else _NullPool() as pool:
+        probe = min(N, 256 * threads)
         t0 = time.perf_counter()
-        one_pass(pool)
-        first = time.perf_counter() - t0
-        passes = max(1, int(seconds / max(first, 1e-9)))
+        run(probe, pool if threads > 1 else None)
+        per_row = (time.perf_counter() - t0) / probe
+        rows = int(min(N, max(probe, seconds / max(per_row, 1e-12))))
+        passes = max(1, int(seconds / max(per_row * N, 1e-12))) if rows == N else 1
         t0 = time.perf_counter()
         for _ in range(passes):
-            one_pass(pool)
+            run(rows, pool if threads > 1 else None)
         elapsed = time.perf_counter() - t0
-    err = float(np.abs(gpu_out.astype(np.float64) - out).max())
-    return {"value": round(passes * work.bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle scalar quantized_matmul split over output columns, {passes} whole passes, "
-                      f"{elapsed:.1f} s on {threads} threads",
+    xbytes = 2 if work.x_dtype == "bf16" else 4
+    pbytes = 2 if work.p_dtype == "bf16" else 4
+    sample_bytes = passes * algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
+    check = min(rows, 512)
+    ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, check))
+    if not np.array_equal(out[:, :check].view(np.uint32), ref[:, :check].view(np.uint32)):
+        raise AssertionError("CPU baseline loop differs from the oracle")
+    err = float(np.abs(gpu_out[:, :rows].astype(np.float64) - out[:, :rows]).max())
+    return {"value": round(sample_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"reference CPU kernel restated (oracle/cpu_baseline.c: scalar, specialised per bits and "
+                       f"dtype pair, ordered f32) over the timed workload, "
+                       + (f"{passes} whole passes" if rows == N else f"rows 0..{rows} of {N} ({rows / N:.1%})")
+                       + f", {elapsed:.1f} s on {threads} thread{'s' if threads > 1 else ''}; host {_cpu_name()}, "
+                         f"nproc {os.cpu_count()}"),
             "max_abs_err_vs_gpu": err}
+
+
+class _NullPool:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
 
 
 def end_to_end(work: Workload, calls: int = 200) -> dict:
@@ -257,6 +273,13 @@ def roofline_gemv(work: Workload, ms: float, traffic) -> dict:
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
 
 
+def roofline_gemm(work: Workload, ms: float, traffic) -> dict:
+    achieved = work.flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+            "workload": work.name, "implementation": work.implementation, "policy": work.policy}
+
+
 def load_traffic(name: str):
     """HBM bytes per launch of the workload's kernel: FETCH_SIZE + WRITE_SIZE
     from counter runs, each scaled by the same counter's reading for a copy of
@@ -272,56 +295,66 @@ LLAMA8B_LAYER = (("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 
                  ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336), ("lm_head", 128256, 4096))
 
 
-def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bool = False) -> dict:
+def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bool = False, sets: int = 2) -> dict:
     """The Llama-8B-shaped projections at 4-bit group 64 (bf16 x, scales and
     biases; one weight seed per projection), run back to back on one stream:
-    a step is the whole sequence. Weights total 4.4 GB per set, larger than
-    the MALL, so no rotation is needed. With ``fused`` the query, key and
-    value projections run as one grouped call and the gate and up projections
-    as one SiLU-gated call (silu(gate) * up written once)."""
+    a step is the whole sequence. One set of the eight weight tensors holds
+    418.9 MB of packed words, scales and biases, more than the 256 MB MALL,
+    and steps alternate between `sets` such sets (838 MB for two), so a
+    step's weights were last touched 838 MB of traffic earlier and come from
+    HBM. With ``fused`` the query, key and value projections run as one
+    grouped call and the gate and up projections as one SiLU-gated call
+    (silu(gate) * up written once)."""
     import affon_amd as A
     from affon_amd import ops
     lib = ops._native.load()
-    calls, impls, nbytes, flops = [], {}, 0, 0
-    tensors, by_name = [], {}
-    for i, (name, N, K) in enumerate(LLAMA8B_LAYER):
-        x = session.randn((M, K), seed=1, dtype="bf16")
-        w = session.randn((N, K), seed=3 + i, std=0.02, dtype="bf16")
-        packed, scales, biases = A.quantize(w, bits=4, group_size=64, param_dtype="bf16")
-        del w
-        by_name[name] = (x, packed, scales, biases)
-        nbytes += algorithmic_bytes(M, N, K, 4, 64, 2, 2)
-        flops += 2 * M * N * K
-        if fused and name in ("k", "v"):
-            # Grouped with q: rebuild the grouped call with every member so far.
-            members = [n for n in ("q", "k", "v") if n in by_name]
-            qx = by_name["q"][0]
-            projections = [by_name[n][1:] for n in members]
-            outs = [session.empty("f32", (M, by_name[n][1].shape[0])) for n in members]
-            descs, epis = ops._grouped_arrays(qx, projections, 4, 64, outs, "auto", "backend_equivalent")
-            calls[0] = (lib.affon_rocm_quantized_matmul_grouped, descs, (epis, len(members)))
-            impls.pop("q", None)
-            impls.pop("q+k", None)
-            impls["+".join(members)] = A.grouped_plan(qx, projections, bits=4, group_size=64)
-            tensors.append((x, packed, scales, biases, outs, descs, epis))
-            continue
-        if fused and name == "up":
-            gx, gp, gs, gb = by_name["gate"]
-            epi = ops._epilogue(up=(packed, scales, biases))
-            calls[-1] = (lib.affon_rocm_quantized_matmul_fused, calls[-1][1], epi)
-            impls["gate+up"] = A.fused_plan(gx, gp, gs, gb, bits=4, group_size=64, up=(packed, scales, biases))
-            del impls["gate"]
-            nbytes -= M * N * 4  # one [M, N] output instead of two
-            tensors.append((x, packed, scales, biases, epi))
-            continue
-        out = session.empty("f32", (M, N))
-        calls.append((lib.affon_rocm_quantized_matmul,
-                       ops._descriptor(x, packed, scales, biases, 4, 64, out, "auto", "backend_equivalent"), None))
-        impls[name] = A.selected_implementation(x, packed, scales, biases, bits=4, group_size=64)
-        tensors.append((x, packed, scales, biases, out))
+    tensors = []
 
-    def launch_all():
-        for fn, desc, epi in calls:
+    def build(copy: int):
+        calls, impls, nbytes, flops = [], {}, 0, 0
+        by_name = {}
+        for i, (name, N, K) in enumerate(LLAMA8B_LAYER):
+            x = session.randn((M, K), seed=1, dtype="bf16")
+            w = session.randn((N, K), seed=3 + i + 100 * copy, std=0.02, dtype="bf16")
+            packed, scales, biases = A.quantize(w, bits=4, group_size=64, param_dtype="bf16")
+            del w
+            by_name[name] = (x, packed, scales, biases)
+            nbytes += algorithmic_bytes(M, N, K, 4, 64, 2, 2)
+            flops += 2 * M * N * K
+            if fused and name in ("k", "v"):
+                # Grouped with q: rebuild the grouped call with every member so far.
+                members = [n for n in ("q", "k", "v") if n in by_name]
+                qx = by_name["q"][0]
+                projections = [by_name[n][1:] for n in members]
+                outs = [session.empty("f32", (M, by_name[n][1].shape[0])) for n in members]
+                descs, epis = ops._grouped_arrays(qx, projections, 4, 64, outs, "auto", "backend_equivalent")
+                calls[0] = (lib.affon_rocm_quantized_matmul_grouped, descs, (epis, len(members)))
+                impls.pop("q", None)
+                impls.pop("q+k", None)
+                impls["+".join(members)] = A.grouped_plan(qx, projections, bits=4, group_size=64)
+                tensors.append((x, packed, scales, biases, outs, descs, epis))
+                continue
+            if fused and name == "up":
+                gx, gp, gs, gb = by_name["gate"]
+                epi = ops._epilogue(up=(packed, scales, biases))
+                calls[-1] = (lib.affon_rocm_quantized_matmul_fused, calls[-1][1], epi)
+                impls["gate+up"] = A.fused_plan(gx, gp, gs, gb, bits=4, group_size=64, up=(packed, scales, biases))
+                del impls["gate"]
+                nbytes -= M * N * 4  # one [M, N] output instead of two
+                tensors.append((x, packed, scales, biases, epi))
+                continue
+            out = session.empty("f32", (M, N))
+            calls.append((lib.affon_rocm_quantized_matmul,
+                          ops._descriptor(x, packed, scales, biases, 4, 64, out, "auto", "backend_equivalent"), None))
+            impls[name] = A.selected_implementation(x, packed, scales, biases, bits=4, group_size=64)
+            tensors.append((x, packed, scales, biases, out))
+        return calls, impls, nbytes, flops
+
+    built = [build(c) for c in range(sets)]
+    impls, nbytes, flops = built[0][1], built[0][2], built[0][3]
+
+    def launch_all(step: int):
+        for fn, desc, epi in built[step % sets][0]:
             if epi is None:
                 status = fn(session._handle, ctypes.byref(desc))
             elif isinstance(epi, tuple):  # grouped: arrays of descriptors and epilogues
@@ -333,36 +366,38 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
                 raise RuntimeError(_native.last_error())
 
     stream = ctypes.c_void_p(session.stream)
-    for _ in range(warmup):
-        launch_all()
+    for i in range(warmup):
+        launch_all(i)
     session.synchronize()
     graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
     hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
-    for _ in range(steps):
-        launch_all()
+    for i in range(steps):
+        launch_all(i)
     hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
     hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
     hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
     session.synchronize()
-    # The median of several timed replays (one replay is `steps` layers): a
-    # single replay varies with the GPU's clock state by several percent.
     start, stop = hip.event(), hip.event()
     times = []
-    for _ in range(5):
+    for _ in range(REPLAYS):
         hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
         hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
         hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
         hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
         ms = ctypes.c_float()
         hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
-        times.append(ms.value)
+        times.append(ms.value / steps)
     hip.lib.hipGraphExecDestroy(exe)
     hip.lib.hipGraphDestroy(graph)
-    t = sorted(times)[len(times) // 2] / steps
+    hip.lib.hipEventDestroy(start)
+    hip.lib.hipEventDestroy(stop)
+    t = sorted(times)[len(times) // 2]
     tensors.clear()
+    built.clear()
     return {"implementations": impls, "us_per_layer": round(t * 1e3, 2),
+            "us_per_layer_replays": [round(v * 1e3, 2) for v in times],
             "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "TFLOP/s": round(flops / (t * 1e-3) / 1e12, 3), "algorithmic_bytes": nbytes}
+            "TFLOP/s": round(flops / (t * 1e-3) / 1e12, 3), "algorithmic_bytes": nbytes, "weight_sets": sets}
 
 
 def copy_calibration(session) -> int:
@@ -403,27 +438,39 @@ def main() -> int:
     if args.copy_calibration:
         return copy_calibration(session)
 
-    main_work = Workload(session, "decode_8bit_g64_m1", 1, 14336, 4096, 8, 64)
-    ms = main_work.time(hip, args.steps, args.warmup, use_graph)
-    gpu_out = main_work.out.numpy()
-    value = main_work.bytes / (ms * 1e-3) / 1e9
-    roofline = roofline_gemv(main_work, ms, load_traffic(main_work.name))
-    impl = main_work.implementation
-    sets = main_work.sets
-    baseline = cpu_baseline(main_work, gpu_out, args.cpu_seconds) if args.cpu_seconds > 0 else None
-    extras = {"decode_8bit_g64_m1_end_to_end": end_to_end(main_work)}
-    if args.cpu_seconds > 0:
-        extras["cpu_baseline_parallel"] = cpu_baseline_parallel(main_work, gpu_out, args.cpu_seconds / 2)
-    main_work.release()
+    def progress(message: str) -> None:
+        print(f"bench: {message}", file=sys.stderr, flush=True)
 
     only = set(filter(None, args.only.split(",")))
 
     def want(name):
         return not only or name in only
 
+    # The reported workload: 4-bit group-64 decode GEMV, 14336 x 4096, M = 1.
+    main_work = Workload(session, "decode_4bit_g64_m1", 1, 14336, 4096, 4, 64)
+    ms = main_work.time(hip, args.steps, args.warmup, use_graph)
+    main_replays = main_work.replay_ms
+    gpu_out = main_work.out.numpy()
+    value = main_work.bytes / (ms * 1e-3) / 1e9
+    roofline = roofline_gemv(main_work, ms, load_traffic(main_work.name))
+    roofline["kernel_us_replays"] = [round(v * 1e3, 3) for v in main_replays]
+    impl = main_work.implementation
+    sets = main_work.sets
+    progress(f"{main_work.name}: {ms * 1e3:.3f} us per step ({roofline['frac']:.1%} of HBM peak)")
+    baseline = None
+    extras = {"decode_4bit_g64_m1_end_to_end": end_to_end(main_work)}
+    if args.cpu_seconds > 0:
+        baseline = cpu_baseline(main_work, gpu_out, args.cpu_seconds)
+        extras["cpu_baseline_all_cores"] = cpu_baseline(main_work, gpu_out, args.cpu_seconds / 2,
+                                                        threads=_host_cores())
+        progress(f"CPU baseline: {baseline['value']} GB/s on 1 thread, "
+                 f"{extras['cpu_baseline_all_cores']['value']} GB/s on {extras['cpu_baseline_all_cores']['cores']}")
+    main_work.release()
+
     def record(name, work, bound="hbm"):
         t = work.time(hip, args.steps, args.warmup, use_graph)
         entry = {"implementation": work.implementation, "us_per_step": round(t * 1e3, 3),
+                 "us_per_step_replays": [round(v * 1e3, 3) for v in work.replay_ms],
                  "GB/s": round(work.bytes / (t * 1e-3) / 1e9, 1),
                  "TFLOP/s": round(work.flops / (t * 1e-3) / 1e12, 3)}
         if bound == "hbm":
@@ -431,23 +478,29 @@ def main() -> int:
         else:
             entry["mfma_frac"] = round(entry["TFLOP/s"] / BF16_MFMA_PEAK_TFLOPS, 4)
         extras[name] = entry
+        progress(f"{name}: {entry['us_per_step']} us per step ({work.implementation})")
         work.release()
+        return t
 
-    for M in (2, 4, 8, 16):
+    for M in (1, 2, 4, 8, 16):
         if want(f"decode_8bit_g64_m{M}"):
             record(f"decode_8bit_g64_m{M}", Workload(session, f"decode_8bit_g64_m{M}", M, 14336, 4096, 8, 64))
-    if want("decode_4bit_g64_m1"):
-        record("decode_4bit_g64_m1", Workload(session, "decode_4bit_g64_m1", 1, 14336, 4096, 4, 64))
+    roofline_prefill = None
     for name, N, K in (("prefill_4bit_g64_m512_n14336_k4096", 14336, 4096),
                        ("prefill_4bit_g64_m512_n4096_k14336", 4096, 14336)):
         if want(name):
-            record(name, Workload(session, name, 512, N, K, 4, 64, policy="approximate"), bound="mfma")
+            work = Workload(session, name, 512, N, K, 4, 64, policy="approximate")
+            t = record(name, work, bound="mfma")
             extras[name]["numerical_policy"] = "approximate"
-    # The same prefill under the default policy (reassociated class: exact codes, the row-tiled MFMA kernel).
-    name = "prefill_4bit_g64_m512_n14336_k4096_backend_equivalent"
-    if want(name):
-        record(name, Workload(session, name, 512, 14336, 4096, 4, 64), bound="mfma")
-        extras[name]["numerical_policy"] = "backend_equivalent"
+            if roofline_prefill is None:
+                roofline_prefill = roofline_gemm(work, t, load_traffic(name))
+                roofline_prefill["kernel_us_replays"] = extras[name]["us_per_step_replays"]
+    # The same prefills under the default policy (backend_equivalent: no rounding of decoded weights).
+    for name, N, K in (("prefill_4bit_g64_m512_n14336_k4096_backend_equivalent", 14336, 4096),
+                       ("prefill_4bit_g64_m512_n4096_k14336_backend_equivalent", 4096, 14336)):
+        if want(name):
+            record(name, Workload(session, name, 512, N, K, 4, 64), bound="mfma")
+            extras[name]["numerical_policy"] = "backend_equivalent"
     # Large prefill stress: 4-bit group 32, 2048 activation rows, both weight orientations.
     for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192", 28672, 8192),
                        ("prefill_4bit_g32_m2048_n8192_k28672", 8192, 28672)):
@@ -457,11 +510,11 @@ def main() -> int:
     if want("decode_4bit_g64_m16"):
         record("decode_4bit_g64_m16", Workload(session, "decode_4bit_g64_m16", 16, 14336, 4096, 4, 64))
     for M in (1, 32):
-        name = f"llama8b_layer_4bit_g64_m{M}"
-        if want(name):
-            extras[name] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup)
-        if want(name + "_fused"):
-            extras[name + "_fused"] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup, fused=True)
+        for fused in (False, True):
+            name = f"llama8b_layer_4bit_g64_m{M}" + ("_fused" if fused else "")
+            if want(name):
+                extras[name] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup, fused=fused)
+                progress(f"{name}: {extras[name]['us_per_layer']} us per layer")
     if want("decode_4bit_g64_f32_4096"):
         record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
                                                     x_dtype="f32", p_dtype="f32"))
@@ -479,11 +532,12 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (Affon seeded generator: x seed 1 N(0,1) bf16, W seed 2 N(0,0.02) quantized on GPU)",
-        "config": {"workload": "decode GEMV 8-bit group 64, W[14336,4096] u32-packed with bf16 scales/biases, "
-                               "x bf16 [1,4096], f32 out", "M": 1, "N": 14336, "K": 4096, "bits": 8,
+        "config": {"workload": "decode GEMV 4-bit group 64, W[14336,4096] u32-packed with bf16 scales/biases, "
+                               "x bf16 [1,4096], f32 out", "M": 1, "N": 14336, "K": 4096, "bits": 4,
                    "group_size": 64, "implementation": impl, "launch": args.launch,
-                   "weight_sets_rotated": sets},
+                   "weight_sets_rotated": sets, "replays": REPLAYS, "timing": "median of the replays"},
         "roofline": roofline,
+        "roofline_prefill": roofline_prefill,
         "cpu_baseline": baseline,
         "extra": extras,
     }

@@ -75,6 +75,14 @@ void oracle_dequantize(const uint32_t* packed, const void* scales, const void* b
                        int param_dtype, size_t N, size_t K, unsigned bits, size_t group_size,
                        int out_dtype, void* out);
 
+/* The CPU baseline (cpu_baseline.c): the same product as
+ * oracle_quantized_matmul, bit for bit, in one specialised scalar loop per
+ * bit width and dtype pair (docs/core/quantized-inference.md:114-128).
+ * Returns 0, or 1 for arguments it does not take. */
+int baseline_quantized_matmul(const void* x, int x_dtype, const uint32_t* packed, const void* scales,
+                              const void* biases, int param_dtype, float* out, size_t M, size_t K, size_t N,
+                              unsigned bits, size_t group_size, size_t n_begin, size_t n_end);
+
 #ifdef __cplusplus
 }
 #endif

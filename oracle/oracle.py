@@ -40,6 +40,8 @@ def load() -> ctypes.CDLL:
                                                 c_size_t, c_size_t, c_size_t, c_uint, c_size_t, c_size_t, c_size_t]
         lib.oracle_quantized_matmul_f64.argtypes = [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                                                     c_size_t, c_size_t, c_size_t, c_uint, c_size_t]
+        lib.baseline_quantized_matmul.restype = c_int
+        lib.baseline_quantized_matmul.argtypes = lib.oracle_quantized_matmul.argtypes
         lib.oracle_quantize.argtypes = [c_void_p, c_int, c_size_t, c_size_t, c_uint, c_size_t, c_int, c_void_p,
                                         c_void_p, c_void_p]
         lib.oracle_dequantize.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_size_t, c_size_t, c_uint, c_size_t,
@@ -97,6 +99,26 @@ def quantized_matmul(x: np.ndarray, packed: np.ndarray, scales: np.ndarray, bias
     load().oracle_quantized_matmul(x.ctypes.data, _code(x), packed.ctypes.data, scales.ctypes.data,
                                    biases.ctypes.data, _code(scales), out.ctypes.data, M, K, N, bits, group_size,
                                    begin, end)
+    return out
+
+
+def baseline_quantized_matmul(x: np.ndarray, packed: np.ndarray, scales: np.ndarray, biases: np.ndarray, bits: int,
+                              group_size: int, n_range: tuple[int, int] | None = None,
+                              out: np.ndarray | None = None) -> np.ndarray:
+    """The CPU baseline loop (cpu_baseline.c): specialised per bit width and
+    dtype pair, bit-identical to quantized_matmul. Releases the GIL while it
+    runs, so threads may split N."""
+    x, packed, scales, biases = _c(x), _c(packed.astype(np.uint32, copy=False)), _c(scales), _c(biases)
+    M, K = x.shape
+    N = packed.shape[0]
+    if out is None:
+        out = np.zeros((M, N), dtype=np.float32)
+    begin, end = n_range if n_range is not None else (0, N)
+    status = load().baseline_quantized_matmul(x.ctypes.data, _code(x), packed.ctypes.data, scales.ctypes.data,
+                                              biases.ctypes.data, _code(scales), out.ctypes.data, M, K, N, bits,
+                                              group_size, begin, end)
+    if status != 0:
+        raise ValueError("baseline_quantized_matmul does not take these arguments")
     return out
 
 

@@ -77,3 +77,75 @@ def assert_close_rtol_atol(actual: np.ndarray, expected: np.ndarray, rtol: float
         i = np.unravel_index(np.argmax(err - bound), err.shape)
         raise AssertionError(f"{int(bad.sum())} of {err.size} elements out of tolerance; worst at {i}: "
                              f"actual {actual[i]!r} expected {expected[i]!r} (rtol {rtol}, atol {atol})")
+
+
+class HipRuntime:
+    """The few HIP runtime calls GPU tests need directly: device memory
+    figures and stream capture into graphs."""
+
+    def __init__(self):
+        import ctypes
+        self.ctypes = ctypes
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        vp, pvp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        psz = ctypes.POINTER(ctypes.c_size_t)
+        for name, args in {"hipMemGetInfo": [psz, psz], "hipStreamBeginCapture": [vp, ctypes.c_int],
+                           "hipStreamEndCapture": [vp, pvp],
+                           "hipGraphInstantiate": [pvp, vp, vp, ctypes.c_char_p, ctypes.c_size_t],
+                           "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp],
+                           "hipStreamSynchronize": [vp]}.items():
+            fn = getattr(self.lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+
+    def check(self, status: int, what: str) -> None:
+        if status != 0:
+            raise RuntimeError(f"{what} failed with HIP status {status}")
+
+    def free_bytes(self) -> int:
+        free, total = self.ctypes.c_size_t(), self.ctypes.c_size_t()
+        self.check(self.lib.hipMemGetInfo(self.ctypes.byref(free), self.ctypes.byref(total)), "hipMemGetInfo")
+        return free.value
+
+    def capture(self, stream: int, enqueue) -> tuple:
+        """Captures what `enqueue()` puts on `stream` into an instantiated graph."""
+        ct = self.ctypes
+        s = ct.c_void_p(stream)
+        graph, exe = ct.c_void_p(), ct.c_void_p()
+        self.check(self.lib.hipStreamBeginCapture(s, 2), "hipStreamBeginCapture")  # relaxed mode
+        try:
+            enqueue()
+        finally:
+            self.check(self.lib.hipStreamEndCapture(s, ct.byref(graph)), "hipStreamEndCapture")
+        self.check(self.lib.hipGraphInstantiate(ct.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+        return graph, exe
+
+    def replay(self, stream: int, graph_exe: tuple) -> None:
+        s = self.ctypes.c_void_p(stream)
+        self.check(self.lib.hipGraphLaunch(graph_exe[1], s), "hipGraphLaunch")
+        self.check(self.lib.hipStreamSynchronize(s), "hipStreamSynchronize")
+
+    def destroy(self, graph_exe: tuple) -> None:
+        self.lib.hipGraphExecDestroy(graph_exe[1])
+        self.lib.hipGraphDestroy(graph_exe[0])
+
+
+def oracle_columns(x, packed, scales, biases, bits: int, group: int, cols, threads: int = 16) -> np.ndarray:
+    """The oracle's output for the given output columns only ([M, len(cols)]):
+    the columns' weight rows are gathered into a smaller problem, which is
+    split over threads (the oracle call releases the interpreter lock)."""
+    from concurrent.futures import ThreadPoolExecutor
+    cols = np.asarray(cols)
+    sub = (np.ascontiguousarray(packed[cols]), np.ascontiguousarray(scales[cols]), np.ascontiguousarray(biases[cols]))
+    out = np.zeros((x.shape[0], len(cols)), dtype=np.float32)
+    parts = max(1, min(threads, len(cols)))
+    bounds = [(len(cols) * i // parts, len(cols) * (i + 1) // parts) for i in range(parts)]
+    with ThreadPoolExecutor(parts) as pool:
+        list(pool.map(lambda r: O.quantized_matmul(x, *sub, bits, group, n_range=r, out=out), bounds))
+    return out
+
+
+def assert_bf16_product_close(actual: np.ndarray, expected: np.ndarray) -> None:
+    """Tolerance for bf16 activations: rtol 1e-2, atol 1e-2 * rms(expected)."""
+    rms = float(np.sqrt(np.mean(expected.astype(np.float64) ** 2)))
+    assert_close_rtol_atol(actual, expected, rtol=1e-2, atol=1e-2 * rms)

@@ -173,3 +173,16 @@ def test_formal_program_authors_one_native_node_and_selects_rocm():
     impl = select_for_specs(specs, {"bits": 8, "group_size": 4}, "backend_equivalent")
     assert impl.startswith("rocm_quantized_matmul") and "host_" not in impl
     assert select_for_specs(specs, {"bits": 8, "group_size": 4}, "exact_only") == "rocm_quantized_matmul.generic"
+
+
+def test_rms_norm_rejects_non_positive_epsilon():
+    """program.ts:578-579: rms_norm needs a finite epsilon > 0 (an all-zero row
+    would otherwise give 0/0). Rejected before any device work."""
+    from affon_amd import program, rms_norm
+    lib = _native.load()
+    for eps in (0.0, -1e-5, float("inf"), float("nan")):
+        assert lib.affon_rocm_rms_norm(None, 4096, _native.F32, 2, 4, eps, 4096) == _native.INVALID_SHAPE, eps
+        assert "invalid rms_norm options" in _native.last_error()
+        with pytest.raises(TypeError, match="invalid rms_norm options"):
+            program("norm", lambda p, eps=eps: rms_norm(p.argument("x", TensorSpec.f32([2, 4])), 1, epsilon=eps))
+    program("norm", lambda p: rms_norm(p.argument("x", TensorSpec.f32([2, 4])), 1, epsilon=1e-6))

@@ -420,3 +420,28 @@ def test_index_select_permutations_and_zero_fill(rng):
     np.testing.assert_array_equal(O.index_select(x, 1, cols), O.index_select(np.ascontiguousarray(x.T), 0, cols).T)
     xb = O.bf16_from_f32(x)
     np.testing.assert_array_equal(O.index_select(xb, 1, cols)[:, 0], xb[:, 4])
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_cpu_baseline_loop_is_bit_identical_to_oracle(bits, rng):
+    """The timed CPU baseline (specialised per bit width and dtype pair) runs
+    the oracle's rounding sequence, so its outputs are the oracle's bit for
+    bit: every dtype pair, power-of-two and odd groups, a group that crosses
+    words, and an N sub-range."""
+    per_word = 32 // bits
+    for x_dtype in ("f32", "bf16"):
+        for p_dtype in ("f32", "bf16"):
+            for M, K, N, group in ((1, 256, 9, 64), (3, per_word * 12, 7, 3 * per_word), (2, per_word * 6, 5, 3)):
+                if K % group:
+                    continue
+                x = storage(rng.standard_normal((M, K)), x_dtype)
+                q = rng.integers(0, 1 << bits, size=(N, K))
+                s = storage(rng.random((N, K // group)) / 16, p_dtype)
+                b = storage(rng.random((N, K // group)) - 0.5, p_dtype)
+                packed = pack_codes(q, bits)
+                want = O.quantized_matmul(x, packed, s, b, bits, group)
+                got = O.baseline_quantized_matmul(x, packed, s, b, bits, group)
+                np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+                part = O.baseline_quantized_matmul(x, packed, s, b, bits, group, n_range=(2, 4))
+                np.testing.assert_array_equal(part[:, 2:4].view(np.uint32), want[:, 2:4].view(np.uint32))
+                assert not part[:, :2].any() and not part[:, 4:].any()
