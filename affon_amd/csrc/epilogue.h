@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <type_traits>
 
 namespace affon {
 
@@ -50,6 +51,31 @@ __device__ __forceinline__ void store_output(const Epilogue& e, float* out, int6
     y = silu(out[idx]) * y;
   }
   out[idx] = y;
+}
+
+// The same for a kind known at compile time (kEpiNone, kEpiBias or
+// kEpiGateMul), p pointing at the element.
+template <int KIND>
+__device__ __forceinline__ void store_as(const Epilogue& e, float* p, int64_t n, float y) {
+  if constexpr (KIND == kEpiBias) {
+    y = y + bias_at(e, n);
+  } else if constexpr (KIND == kEpiGateMul) {
+    y = silu(*p) * y;
+  }
+  *p = y;
+}
+
+// Calls f(std::integral_constant<int, KIND>) for the stored kind, branching
+// once: kernels that store many elements per thread emit one straight-line
+// store sequence per kind instead of a branch per element.
+template <class F>
+__device__ __forceinline__ void with_store_kind(int kind, F&& f) {
+  if (kind == kEpiBias)
+    f(std::integral_constant<int, kEpiBias>{});
+  else if (kind == kEpiGateMul)
+    f(std::integral_constant<int, kEpiGateMul>{});
+  else
+    f(std::integral_constant<int, kEpiNone>{});
 }
 
 }  // namespace affon

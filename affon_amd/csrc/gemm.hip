@@ -273,26 +273,32 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_kernel(TileArgs a) {
   wait_vmcnt<0>();
 
   // Accumulator (mt, nt) element v of lane l is row 8*(v/4) + 4*(l/32) + v%4
-  // and column l%32 of its 32x32 tile.
-  auto for_each_output = [&](auto&& f) {
+  // and column l%32 of its 32x32 tile. Offsets are 32-bit from the tile's
+  // first output row (128 rows * N * 4 < 2^31), and the epilogue kind is
+  // branched on once.
+  const bool full = m0 + kBM <= a.M;  // no row checks for whole tiles
+  float* base = (a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N) +
+                static_cast<int64_t>(m0) * a.N;
+  with_store_kind(a.splits == 1 ? a.epi.kind : kEpiNone, [&](auto kind) {
+    constexpr int KIND = decltype(kind)::value;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int col = n0 + 32 * nt + li;
+      if (col < a.N) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = m0 + 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
-          if (row < a.M && col < a.N) f(static_cast<int64_t>(row) * a.N + col, col, acc[mt][nt][v]);
-        }
+          for (int v = 0; v < 16; ++v) {
+            const int r = 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
+            if (full || m0 + r < a.M) {
+              const uint32_t off = static_cast<uint32_t>(r * a.N + col) * 4u;
+              store_as<KIND>(a.epi, reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(base) + off), col,
+                             acc[mt][nt][v]);
+            }
+          }
+      }
     }
-  };
-  if (a.splits == 1) {
-    for_each_output([&](int64_t i, int col, float v) { store_output(a.epi, a.out, i, col, v); });
-  } else {
-    float* dst = a.partial + split * static_cast<int64_t>(a.M) * a.N;
-    for_each_output([&](int64_t i, int, float v) { dst[i] = v; });
-  }
+  });
 }
 
 template <int BITS, typename PT>
@@ -321,12 +327,14 @@ bool mfma_supports(const QmmProblem& p) {
   if (reinterpret_cast<uintptr_t>(p.s) % 4 != 0 || reinterpret_cast<uintptr_t>(p.b) % 4 != 0) return false;
   if ((p.ss0 * pbytes) % 4 != 0 || (p.bs0 * pbytes) % 4 != 0 || (p.K / p.group * pbytes) % 4 != 0) return false;
   if (4 * kBK / p.group > 16 / pbytes) return false;
-  if (p.M > (int64_t(1) << 30) || p.N > (int64_t(1) << 30) || p.K > (int64_t(1) << 30)) return false;
+  // 128 rows * N * 4 bytes of output offsets fit in 31 bits.
+  if (p.M > (int64_t(1) << 30) || p.N > (int64_t(1) << 22) || p.K > (int64_t(1) << 30)) return false;
   if (((p.N + kBN - 1) / kBN) * ((p.M + kBM - 1) / kBM) > (int64_t(1) << 31) - 1) return false;
   return true;
 }
 
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
+  if (p.M > 128 && pair_supports(p)) return pair_launch(p, l);
   hipStream_t stream = l.stream;
   TileArgs a;
   a.x = reinterpret_cast<const uint16_t*>(p.x);

@@ -278,16 +278,26 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
       for (int i = 0; i < 4; ++i) ysum(wave)[(16 * rb + 4 * h + i) * kCols + 16 * ct + r] = y[rb][ct][i];
   __syncthreads();
   float* dst = a.partial + split * static_cast<int64_t>(a.M) * pstride;
+  if (a.splits == 1) {
+    with_store_kind(a.epi.kind, [&](auto kind) {
+      constexpr int KIND = decltype(kind)::value;
 #pragma unroll
-  for (int e = 0; e < kRows * kCols / kThreads; ++e) {
-    const int o = e * kThreads + tid;
-    const int row = m0 + o / kCols, col = n0 + o % kCols;
-    if (row < a.M && col < a.N) {
-      const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
-      if (a.splits == 1)
-        store_output(a.epi, a.out, static_cast<int64_t>(row) * a.N + col, col, v);
-      else
-        dst[static_cast<int64_t>(row) * pstride + col_base + col] = v;
+      for (int e = 0; e < kRows * kCols / kThreads; ++e) {
+        const int o = e * kThreads + tid;
+        const int row = m0 + o / kCols, col = n0 + o % kCols;
+        if (row < a.M && col < a.N) {
+          const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
+          store_as<KIND>(a.epi, a.out + static_cast<int64_t>(row) * a.N + col, col, v);
+        }
+      }
+    });
+  } else {
+#pragma unroll
+    for (int e = 0; e < kRows * kCols / kThreads; ++e) {
+      const int o = e * kThreads + tid;
+      const int row = m0 + o / kCols, col = n0 + o % kCols;
+      if (row < a.M && col < a.N)
+        dst[static_cast<int64_t>(row) * pstride + col_base + col] = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
     }
   }
 }

@@ -88,6 +88,11 @@ hipError_t gemv_mfma_group_launch(const QmmProblem* group, int count, const Laun
 
 bool mfma_supports(const QmmProblem& p);
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l);
+// The 4-bit prefill kernel whose column-sharing waves split the decode
+// (gemm_pair.hip); mfma_launch runs it for the shapes it takes with more
+// than 128 rows.
+bool pair_supports(const QmmProblem& p);
+hipError_t pair_launch(const QmmProblem& p, const Launch& l);
 
 hipError_t quantize_launch(const void* weights, int weight_dtype, int64_t rows, int64_t columns,
                            int bits, int64_t group, uint32_t* packed, void* scales, void* biases,
