@@ -69,7 +69,38 @@ void* Workspace::get(size_t bytes) {
 
 }  // namespace affon
 
+// Scratch memory of affon_rocm_quantized_matmul_noalloc: the split-K partial
+// sums of the tiled kernels, in a static device array (one per GPU, held
+// until the process ends). Host code uses only the per-device address that
+// hipGetSymbolAddress returns for it (kept by scratch_on), never the array's
+// name, which on the host is a stand-in and not a device address.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
+
+// Device address of `scratch` on `device`, looked up once per device with the
+// device current (at session creation); nullptr when the lookup failed.
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[64] = {};
+bool g_scratch_done[64] = {};
+
+hipError_t scratch_setup(int device) {
+  if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_done[device]) return g_scratch_ptr[device] != nullptr ? hipSuccess : hipErrorInvalidSymbol;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  g_scratch_done[device] = true;
+  g_scratch_ptr[device] = e == hipSuccess ? ptr : nullptr;
+  return e;
+}
+
+void* scratch_on(int device) {
+  if (device < 0 || device >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  return g_scratch_ptr[device];
+}
 
 thread_local std::string g_last_error;
 
@@ -293,6 +324,11 @@ int affon_rocm_session_create(int device, affon_rocm_session** out) {
   if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   hipStream_t stream = nullptr;
   if ((e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)) != hipSuccess) return hip_fail(e, "hipStreamCreate");
+  // The no-allocation entry point's scratch address on this device.
+  if ((e = scratch_setup(device)) != hipSuccess) {
+    (void)hipStreamDestroy(stream);
+    return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  }
   auto* session = new affon_rocm_session;
   session->device = device;
   session->stream = stream;
@@ -397,6 +433,31 @@ int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qm
   launch.stream = session->stream;
   launch.workspace = session->workspace;
   hipError_t e = c->launch(p, launch);
+  if (e != hipSuccess) return hip_fail(e, c->id);
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon_rocm_qmm_desc* desc) {
+  clear_error();
+  affon::QmmProblem p;
+  int status = validate(desc, &p);
+  if (status != AFFON_ROCM_OK) return status;
+  const Candidate* c = nullptr;
+  if ((status = select(desc, p, &c)) != AFFON_ROCM_OK) return status;
+  if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
+  void* fixed = scratch_on(session->device);
+  if (fixed == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "no-allocation scratch is not set up on device %d",
+                                    session->device);
+  affon::Launch launch;
+  launch.stream = session->stream;
+  launch.fixed = fixed;
+  launch.fixed_bytes = kNoAllocScratchBytes;
+  hipError_t e = c->launch(p, launch);
+  if (launch.fixed_short > 0)
+    return fail(AFFON_ROCM_UNSUPPORTED,
+                "%s needs %zu bytes of split-K scratch for this shape, more than the %zu bytes the no-allocation "
+                "entry point holds; use affon_rocm_quantized_matmul",
+                c->id, launch.fixed_short, kNoAllocScratchBytes);
   if (e != hipSuccess) return hip_fail(e, c->id);
   return AFFON_ROCM_OK;
 }

@@ -357,12 +357,14 @@ hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
   a.splits = 1;
   a.split_steps = steps;
   a.partial = nullptr;
-  const int splits = l.workspace != nullptr ? choose_splits(tiles, steps) : 1;
+  const int splits = l.can_split() ? choose_splits(tiles, steps) : 1;
   if (splits > 1) {
-    if (auto* ws = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * p.N * 4))) {
+    if (auto* ws = static_cast<float*>(l.scratch(static_cast<size_t>(splits) * p.M * p.N * 4))) {
       a.splits = splits;
       a.split_steps = steps / splits;
       a.partial = ws;
+    } else if (l.fixed != nullptr) {
+      return hipErrorOutOfMemory;  // the fixed scratch buffer cannot hold this plan's partial sums
     }
   }
   const bool bf16p = p.p_dtype == AFFON_ROCM_BF16;

@@ -423,13 +423,15 @@ hipError_t tiled_launch(const QmmProblem& p, const QmmProblem* group, int count,
   // least two chunks.
   const int row_tiles = static_cast<int>((p.M + kMaxRows - 1) / kMaxRows);
   int splits = 1;
-  if (l.workspace != nullptr)
+  if (l.can_split())
     while (splits < 8 && tiles * row_tiles * splits < device_cus() * 3 / 4 && chunks >= 2 * kWaves * 2 * splits)
       splits *= 2;
   if (splits > 1) {
-    if (auto* w = static_cast<float*>(l.workspace->get(static_cast<size_t>(splits) * p.M * columns * 4))) {
+    if (auto* w = static_cast<float*>(l.scratch(static_cast<size_t>(splits) * p.M * columns * 4))) {
       a.splits = splits;
       a.partial = w;
+    } else if (l.fixed != nullptr) {
+      return hipErrorOutOfMemory;  // the fixed scratch buffer cannot hold this plan's partial sums
     }
   }
   const bool bf16p = p.p_dtype == AFFON_ROCM_BF16;

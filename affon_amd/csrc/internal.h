@@ -54,10 +54,27 @@ class Workspace {
   size_t retired_bytes_ = 0;  // size of the last retired buffer
 };
 
-// Where a launcher enqueues its work.
+// Where a launcher enqueues its work, and the scratch memory it may use for
+// split-K partial sums: the session's workspace (grown on demand), or a
+// fixed buffer of fixed_bytes (the no-allocation entry point), or none.
 struct Launch {
   hipStream_t stream = nullptr;
-  Workspace* workspace = nullptr;  // may be null: launchers then use no scratch memory
+  Workspace* workspace = nullptr;
+  void* fixed = nullptr;
+  size_t fixed_bytes = 0;
+  // Set when a fixed buffer is too small for the launcher's plan; the
+  // launcher then launches nothing and returns hipErrorOutOfMemory.
+  mutable size_t fixed_short = 0;
+
+  bool can_split() const { return workspace != nullptr || fixed != nullptr; }
+  // At least `bytes` of scratch, or nullptr (workspace: it cannot grow now;
+  // fixed buffer: too small, recorded in fixed_short).
+  void* scratch(size_t bytes) const {
+    if (workspace != nullptr) return workspace->get(bytes);
+    if (fixed != nullptr && bytes <= fixed_bytes) return fixed;
+    if (fixed != nullptr) fixed_short = bytes;
+    return nullptr;
+  }
 };
 
 // Per-candidate capability guards and launchers. A guard returns true when

@@ -124,6 +124,20 @@ const char* affon_rocm_last_error(void);
  * OpTag.quantized_matmul (src/js/compute/native.zig:1406). */
 int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qmm_desc* desc);
 
+/* The same operation without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * split-K partial sums that affon_rocm_quantized_matmul keeps in the
+ * session's growable workspace go instead to a static 32 MiB device array
+ * (one per GPU, held until the process ends), whose address is looked up
+ * once per device when a session is created. Same selection, kernels and
+ * results as affon_rocm_quantized_matmul; a shape whose split-K plan needs
+ * more than 32 MiB of partial sums is rejected with AFFON_ROCM_UNSUPPORTED
+ * before anything is enqueued (the output is untouched). Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (other streams,
+ * other sessions, other threads) race. */
+int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon_rocm_qmm_desc* desc);
+
 /* Runs validation and selection only and writes the selected implementation
  * id (e.g. "rocm_quantized_matmul.gemv") into id (capacity cap, NUL-terminated).
  * Mirrors the compiler's implementation_id in executable explanations

@@ -1,0 +1,67 @@
+"""affon_rocm_quantized_matmul_noalloc through the C ABI: the same kernels
+with split-K partial sums in the library's static scratch array instead of
+the session workspace. Each call is checked against affon_rocm_quantized_matmul
+on the same operands. The bar is bit-identical outputs: the same plan runs
+and the split-K sums are added in a fixed order. Two calls run in a row, the
+second on a smaller problem, so the second reuses the array the first left
+behind. A shape whose plan needs more than the array holds must be rejected
+before anything is launched, leaving its output untouched."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import affon_amd as A
+from affon_amd import _native, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def problem(session, M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    x = session.from_bytes(A.core.bf16_bits(rng.standard_normal((M, K)).astype(np.float32)), A.TensorSpec.bf16((M, K)))
+    w = session.from_bytes(rng.integers(0, 1 << 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32),
+                           A.TensorSpec.u32((N, K // 8)))
+    s = session.from_bytes(A.core.bf16_bits((0.008 + 0.004 * rng.random((N, K // 64))).astype(np.float32)),
+                           A.TensorSpec.bf16((N, K // 64)))
+    b = session.from_bytes(A.core.bf16_bits((-0.06 + 0.02 * rng.random((N, K // 64))).astype(np.float32)),
+                           A.TensorSpec.bf16((N, K // 64)))
+    return x, w, s, b
+
+
+def run(session, entry, operands, policy):
+    x, w, s, b = operands
+    out = session.tensor(np.full((x.shape[0], w.shape[0]), 7.0, np.float32))
+    desc = ops._descriptor(x, w, s, b, 4, 64, out, "auto", policy)
+    status = getattr(_native.load(), entry)(session._handle, ctypes.byref(desc))
+    message = _native.last_error()  # before the synchronize clears it
+    session.synchronize()
+    return status, out.numpy(), message
+
+
+def test_noalloc_matches_allocating_entry_point():
+    with A.Session("rocm") as session:
+        lib = _native.load()
+        cases = [
+            # prefill whose four K ranges fill the whole array: 4 x 512 x 4096 f32 = 32 MiB
+            ((512, 4096, 14336), "approximate", "rocm_quantized_matmul.mfma"),
+            # a smaller decode batch with split K, reusing what the first call left in the array
+            ((16, 4096, 4096), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma"),
+        ]
+        for (M, N, K), policy, impl in cases:
+            operands = problem(session, M, N, K, seed=M + N)
+            assert A.selected_implementation(*operands, bits=4, group_size=64, policy=policy) == impl
+            want_status, want, _ = run(session, "affon_rocm_quantized_matmul", operands, policy)
+            got_status, got, message = run(session, "affon_rocm_quantized_matmul_noalloc", operands, policy)
+            assert want_status == 0 and got_status == 0, message
+            assert np.isfinite(got).all()
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=f"{M}x{N}x{K}")
+        # 1280 x 4096 prefill: two K ranges of 1280 x 4096 f32 partial sums (42 MB) exceed the array.
+        operands = problem(session, 1280, 4096, 4096, seed=3)
+        status, out, message = run(session, "affon_rocm_quantized_matmul_noalloc", operands, "approximate")
+        assert status == _native.UNSUPPORTED
+        assert "no-allocation" in message and "scratch" in message, message
+        np.testing.assert_array_equal(out, np.full(out.shape, 7.0, np.float32))
+        # The allocating entry point runs it.
+        status, out, message = run(session, "affon_rocm_quantized_matmul", operands, "approximate")
+        assert status == 0 and np.isfinite(out).all(), message
