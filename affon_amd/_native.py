@@ -76,6 +76,8 @@ SIGNATURES = {
     "affon_rocm_last_error": (c_char_p, []),
     "affon_rocm_quantized_matmul": (c_int, [c_void_p, ctypes.POINTER(QmmDesc)]),
     "affon_rocm_quantized_matmul_noalloc": (c_int, [c_void_p, ctypes.POINTER(QmmDesc)]),
+    "affon_rocm_read_floor": (c_int, [c_void_p, ctypes.POINTER(c_void_p), ctypes.POINTER(ctypes.c_uint64), c_int,
+                                      c_void_p]),
     "affon_rocm_quantized_matmul_select": (c_int, [ctypes.POINTER(QmmDesc), c_char_p, c_size_t]),
     "affon_rocm_quantized_matmul_fused": (c_int, [c_void_p, ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue)]),
     "affon_rocm_quantized_matmul_fused_select": (c_int, [ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue), c_char_p,

@@ -462,6 +462,22 @@ int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon
   return AFFON_ROCM_OK;
 }
 
+int affon_rocm_read_floor(affon_rocm_session* session, const void* const* buffers, const uint64_t* bytes, int count,
+                          void* sink) {
+  clear_error();
+  if (buffers == nullptr || bytes == nullptr || sink == nullptr || count < 1 || count > 4)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor needs 1 to 4 buffers, their sizes and a sink word");
+  for (int i = 0; i < count; ++i) {
+    if (buffers[i] == nullptr || reinterpret_cast<uintptr_t>(buffers[i]) % 16 != 0 || bytes[i] < 16)
+      return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor buffer %d is null, unaligned or shorter than 16 bytes", i);
+  }
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::read_floor_launch(buffers, bytes, count, static_cast<uint32_t*>(sink), session->stream);
+  if (e != hipSuccess) return hip_fail(e, "read_floor");
+  return AFFON_ROCM_OK;
+}
+
 int affon_rocm_quantized_matmul_select(const affon_rocm_qmm_desc* desc, char* id, size_t cap) {
   clear_error();
   affon::QmmProblem p;

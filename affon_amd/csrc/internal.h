@@ -119,6 +119,10 @@ hipError_t rms_norm_launch(const void* x, int dtype, int64_t rows, int64_t cols,
 hipError_t softmax_launch(const void* x, int dtype, int64_t rows, int64_t cols, void* out, hipStream_t stream);
 hipError_t index_select_launch(const void* x, int dtype, int64_t rows, int64_t cols, int axis, const int64_t* index,
                                int64_t count, void* out, hipStream_t stream);
+// One launch that reads every whole 16-byte chunk of up to four buffers once
+// (diag.hip); sink receives at most one word.
+hipError_t read_floor_launch(const void* const* buffers, const uint64_t* bytes, int count, uint32_t* sink,
+                             hipStream_t stream);
 hipError_t dequantize_launch(const uint32_t* packed, const void* scales, const void* biases,
                              int param_dtype, int64_t rows, int64_t columns, int bits, int64_t group,
                              void* out, int out_dtype, hipStream_t stream);

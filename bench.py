@@ -160,6 +160,51 @@ class Workload:
         self.replay_ms = runs
         return sorted(runs)[len(runs) // 2]
 
+    def time_read_floor(self, hip: Hip, steps: int, warmup: int) -> float:
+        """Milliseconds per launch of affon_rocm_read_floor over the same
+        rotated weight sets (packed words, scales, biases): the median of
+        REPLAYS graph replays of `steps` launches, as for the workload."""
+        sink = self.session.empty("u32", (4,))
+        calls = []
+        for packed, scales, biases in self.weights:
+            ptrs = (ctypes.c_void_p * 3)(packed.data_ptr, scales.data_ptr, biases.data_ptr)
+            sizes = (ctypes.c_uint64 * 3)(packed._buffer.nbytes, scales._buffer.nbytes, biases._buffer.nbytes)
+            calls.append((ptrs, sizes))
+
+        def launch(i):
+            ptrs, sizes = calls[i % len(calls)]
+            if self.lib.affon_rocm_read_floor(self.session._handle, ptrs, sizes, 3, sink.data_ptr) != 0:
+                from affon_amd import _native
+                raise RuntimeError(_native.last_error())
+
+        stream = ctypes.c_void_p(self.session.stream)
+        for i in range(warmup):
+            launch(i)
+        self.session.synchronize()
+        graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+        hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+        for i in range(steps):
+            launch(i)
+        hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+        hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+        self.session.synchronize()
+        start, stop = hip.event(), hip.event()
+        runs = []
+        for _ in range(REPLAYS):
+            hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+            hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+            hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+            hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+            ms = ctypes.c_float()
+            hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+            runs.append(ms.value / steps)
+        hip.lib.hipGraphExecDestroy(exe)
+        hip.lib.hipGraphDestroy(graph)
+        hip.lib.hipEventDestroy(start)
+        hip.lib.hipEventDestroy(stop)
+        return sorted(runs)[len(runs) // 2]
+
     def host_operands(self):
         packed, scales, biases = self.weights[0]
         return self.x.storage(), packed.storage(), scales.storage(), biases.storage()
@@ -456,7 +501,18 @@ def main() -> int:
     roofline["kernel_us_replays"] = [round(v * 1e3, 3) for v in main_replays]
     impl = main_work.implementation
     sets = main_work.sets
-    progress(f"{main_work.name}: {ms * 1e3:.3f} us per step ({roofline['frac']:.1%} of HBM peak)")
+    # The floor of a launch that only reads the same weight bytes (no decode,
+    # no activations, no output): the decode's distance from it is its overhead.
+    floor_ms = main_work.time_read_floor(hip, args.steps, args.warmup)
+    weight_bytes = main_work.bytes - main_work.M * main_work.K * 2 - main_work.M * main_work.N * 4
+    roofline["read_floor"] = {"us": round(floor_ms * 1e3, 3), "weight_bytes": weight_bytes,
+                              "GB/s": round(weight_bytes / (floor_ms * 1e-3) / 1e9, 1),
+                              "frac_of_peak": round(weight_bytes / (floor_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "decode_over_floor": round(ms / floor_ms, 4),
+                              "kernel": "affon_rocm_read_floor (read_kernel: reads the packed words, scales and "
+                                        "biases once, same rotation and graph replays)"}
+    progress(f"{main_work.name}: {ms * 1e3:.3f} us per step ({roofline['frac']:.1%} of HBM peak); "
+             f"read floor {floor_ms * 1e3:.3f} us")
     baseline = None
     extras = {"decode_4bit_g64_m1_end_to_end": end_to_end(main_work)}
     if args.cpu_seconds > 0:

@@ -138,6 +138,15 @@ int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qm
  * other sessions, other threads) race. */
 int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon_rocm_qmm_desc* desc);
 
+/* Measurement helper, no counterpart in the reference: enqueues one launch
+ * that reads every whole 16-byte chunk of `count` (1..4) 16-byte-aligned
+ * device buffers once and nothing else, with the geometry of the M = 1
+ * decode kernel (256-thread workgroups, four 16-byte loads per lane issued
+ * before any wait). Its period is the floor a decode launch reading the same
+ * weights can reach. `sink` (one device word) is written at most once. */
+int affon_rocm_read_floor(affon_rocm_session* session, const void* const* buffers, const uint64_t* bytes, int count,
+                          void* sink);
+
 /* Runs validation and selection only and writes the selected implementation
  * id (e.g. "rocm_quantized_matmul.gemv") into id (capacity cap, NUL-terminated).
  * Mirrors the compiler's implementation_id in executable explanations
