@@ -107,11 +107,16 @@ struct RowBlocks {
   static constexpr int kBlocks = XROWS > 16 ? 2 : 1;  // blocks of 16 MFMA rows
   static constexpr int kRows = 16 * kBlocks;           // rows with results
 };
-template <int BITS, typename PT, int XROWS>
+//
+// PWHOLE: the scales and biases of a wave's whole K range arrive once, in
+// the prologue (issued before any other transfer, so every later wait covers
+// them), when they fit 32 bytes per column (e.g. 16 groups of bf16); this
+// cuts their memory requests by the number of 4-step windows.
+template <int BITS, typename PT, int XROWS, bool PWHOLE>
 __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   TileArgs a = args;
   constexpr int kXLoads = XROWS / 8;  // activation DMA instructions per step
-  using P = Plan<BITS, PT, kXLoads>;
+  using P = Plan<BITS, PT, kXLoads, PWHOLE>;
   constexpr int RB = RowBlocks<XROWS>::kBlocks;
   constexpr int kRows = RowBlocks<XROWS>::kRows;
   __shared__ __attribute__((aligned(16))) uint8_t lds_x[kWaves][kStages][XROWS * 128];
@@ -168,10 +173,13 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     for (int i = 0; i < kXLoads; ++i)
       load_lds<16>(x_src[i] + (s0 + step) * kBK, lds_address(lds_x[wave][step & 3]) + 1024 * i);
   };
-  WeightStream<BITS, PT, kXLoads> ws;
-  ws.init(a, n0, s0, lane, lds_w[0][wave], kWaves * P::kWBytes, lds_p[0][wave], kWaves * P::kPBytes);
+  WeightStream<BITS, PT, kXLoads, PWHOLE> ws;
+  // PWHOLE keeps one window per wave: both window buffers of the wave, which
+  // are adjacent when indexed [wave][buffer].
+  uint8_t* p_base = PWHOLE ? lds_p[0][0] + wave * 2 * P::kPBytes : lds_p[0][wave];
+  ws.init(a, n0, s0, lane, lds_w[0][wave], kWaves * P::kWBytes, p_base, kWaves * P::kPBytes);
   auto issue_all = [&](int j, int pstep, int wstep, int astep) {
-    if (j == 0)
+    if (j == 0 && !PWHOLE)
       for (int i = 0; i < P::kPLoads; ++i) ws.issue_p(pstep, i);
     if (P::kStepsPerW == 1 || j == 0)
       for (int i = 0; i < P::kWLoads; ++i) ws.issue_w(wstep, i);
@@ -253,6 +261,10 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   }
 
   if (steps > 0) {
+    if constexpr (PWHOLE) {
+#pragma unroll
+      for (int i = 0; i < P::kPWholeLoads; ++i) ws.issue_p_whole(i);
+    }
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) issue_all(rr, 0, min(rr, last), min(max(rr - 1, 0), last));
     for (int t = 0; t < steps;) {
@@ -302,16 +314,43 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   }
 }
 
+// Whether every wave's scales and biases fit one whole-range window of 32
+// bytes per column: the dwords from the one holding a wave's first group
+// through the one holding its last, for every K range and wave.
+template <typename PT>
+bool whole_range_params(const TileArgs& a) {
+  const int chunks = a.K / (4 * kBK);
+  for (int split = 0; split < a.splits; ++split) {
+    const int g0 = split * chunks / a.splits, g1 = (split + 1) * chunks / a.splits;
+    for (int w = 0; w < kWaves; ++w) {
+      const int c0 = g0 + w * (g1 - g0) / kWaves, c1 = g0 + (w + 1) * (g1 - g0) / kWaves;
+      if (c1 <= c0) continue;
+      const int64_t first = (int64_t(4 * c0) * kBK >> (5 + a.group_shift)) * PT::bytes / 4;
+      const int64_t last = ((int64_t(4 * c1) * kBK - 1) >> (5 + a.group_shift)) * PT::bytes / 4;
+      if (last - first + 1 > 8) return false;
+    }
+  }
+  return true;
+}
+
+template <int BITS, typename PT, bool PWHOLE>
+void launch_skinny(const TileArgs& args, dim3 grid, hipStream_t stream) {
+  if (args.M <= 8)
+    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 8, PWHOLE>), grid, dim3(kThreads), 0, stream, args);
+  else if (args.M <= 16)
+    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 16, PWHOLE>), grid, dim3(kThreads), 0, stream, args);
+  else
+    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 32, PWHOLE>), grid, dim3(kThreads), 0, stream, args);
+}
+
 template <int BITS, typename PT>
 hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
   const int tiles = args.seg.count > 0 ? args.seg.total_tiles : (args.N + kCols - 1) / kCols;
   const dim3 grid(tiles * args.splits, (args.M + kMaxRows - 1) / kMaxRows);
-  if (args.M <= 8)
-    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 8>), grid, dim3(kThreads), 0, stream, args);
-  else if (args.M <= 16)
-    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 16>), grid, dim3(kThreads), 0, stream, args);
+  if (whole_range_params<PT>(args))
+    launch_skinny<BITS, PT, true>(args, grid, stream);
   else
-    hipLaunchKernelGGL((qskinny_kernel<BITS, PT, 32>), grid, dim3(kThreads), 0, stream, args);
+    launch_skinny<BITS, PT, false>(args, grid, stream);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || args.splits == 1) return e;
   return launch_reduce(args, stream);

@@ -140,7 +140,10 @@ struct Unroll<N, N> {
 };
 
 // Transfer plan of one wave (64 weight columns) for a weight format, with
-// ALOADS activation transfer instructions per step and wave.
+// ALOADS activation transfer instructions per step and wave. With PWHOLE the
+// scales and biases of the wave's whole K range arrive once, before the
+// first step, instead of a window every four steps (WeightStream::
+// issue_p_whole; the caller checks that the range fits kPWholeBytes).
 //
 // Packed words reach LDS in runs of kColBytes per column: four K steps at a
 // time for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per column), one step at a
@@ -153,7 +156,7 @@ struct Unroll<N, N> {
 // groups, f32: 4 groups), starting at the dword that holds the first group of
 // those 256 k values, which covers all of their groups for the group sizes
 // the kernel accepts; dwords past the row end repeat the row's last dword.
-template <int BITS, typename PT, int ALOADS>
+template <int BITS, typename PT, int ALOADS, bool PWHOLE = false>
 struct Plan {
   static constexpr int kStepsPerW = BITS == 8 ? 1 : 4;           // steps per packed-word transfer
   static constexpr int kColBytes = 8 * BITS * kStepsPerW;         // bytes per column per transfer
@@ -164,6 +167,9 @@ struct Plan {
   static constexpr int kPLoads = 8;                               // 4-byte DMA: 4 for scales, 4 for biases
   static constexpr int kPBytes = 2 * 64 * 16;                     // per wave and buffer: 16-byte windows of scales, biases
   static constexpr int kALoads = ALOADS;                          // activation DMA instructions per step
+  static constexpr int kPWholeBytes = 32;                         // per column and parameter (PWHOLE)
+  static constexpr int kPWholeLoads = 2 * 64 * kPWholeBytes / 256;  // 4-byte DMA instructions (PWHOLE)
+  static_assert(2 * 64 * kPWholeBytes <= 2 * kPBytes, "whole-range parameters fit the window buffers");
 
   // Slot (16-byte unit) holding part `part` of column c's run. 128-byte runs:
   // within 8 consecutive columns the slots differ; columns c and c+8 (same
@@ -177,7 +183,7 @@ struct Plan {
   // Transfers issued by iteration j (= step index mod 4), in issue order
   // parameters, words, activations; group 0 = parameters, 1 = words, 2 = activations.
   static constexpr int group_ops(int j, int g) {
-    return g == 0 ? (j == 0 ? kPLoads : 0) : g == 1 ? (kStepsPerW == 1 || j == 0 ? kWLoads : 0) : kALoads;
+    return g == 0 ? (j == 0 && !PWHOLE ? kPLoads : 0) : g == 1 ? (kStepsPerW == 1 || j == 0 ? kWLoads : 0) : kALoads;
   }
   static constexpr int ops(int j) { return group_ops(j, 0) + group_ops(j, 1) + group_ops(j, 2); }
   // Transfers issued after group g of the iteration r iterations before one
@@ -198,7 +204,7 @@ struct Plan {
     const int rp = j == 3 ? 3 : j + 4;
     const int nw = ops_after(j, rw, 1), np = ops_after(j, rp, 0);
     n = nw < n ? nw : n;
-    n = np < n ? np : n;
+    if (!PWHOLE) n = np < n ? np : n;  // whole-range parameters precede every transfer waited for
     return n;
   }
   static_assert(kWLoads * 1024 == kWBytes, "whole DMA instructions");
@@ -209,12 +215,16 @@ struct Plan {
 // the wave's slices of a ring of LDS buffers: w_lds(buf) = w_base + buf *
 // w_stride (Plan::kWBufs buffers of kWBytes), p_lds(buf) likewise (2 buffers
 // of kPBytes). Steps passed to the methods are local to the K range.
-template <int BITS, typename PT, int ALOADS>
+template <int BITS, typename PT, int ALOADS, bool PWHOLE = false>
 struct WeightStream {
-  using P = Plan<BITS, PT, ALOADS>;
+  using P = Plan<BITS, PT, ALOADS, PWHOLE>;
   const uint8_t* w_src[P::kWLoads];
   const uint8_t* s_col[4];
   const uint8_t* b_col[4];
+  const uint8_t* s_whole;  // PWHOLE: parameter tensors, their row strides in bytes, the columns
+  const uint8_t* b_whole;
+  int64_t s_row_bytes, b_row_bytes;
+  int n0_, n_cols;
   uint8_t* w_base;
   uint8_t* p_base;
   int w_stride, p_stride;
@@ -243,6 +253,12 @@ struct WeightStream {
     // Parameter windows: DMA lane L of instruction i carries dword L%4 of the
     // window of local column 16i + L/4, stored at byte 16*(16i + L/4) + 4*(L%4).
     row_dwords = (a.K >> (5 + a.group_shift)) * PT::bytes / 4;  // whole dwords per parameter row
+    s_whole = a.s;
+    b_whole = a.b;
+    s_row_bytes = a.ss0 * PT::bytes;
+    b_row_bytes = a.bs0 * PT::bytes;
+    n0_ = n0;
+    n_cols = a.N;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int col = min(n0 + 16 * i + (lane >> 2), a.N - 1);
@@ -253,6 +269,19 @@ struct WeightStream {
   // First dword of the parameter window for the four global steps starting at gstep.
   __device__ __forceinline__ int window(int gstep) const {
     return (((gstep * kBK) >> (5 + group_shift)) * PT::bytes) >> 2;
+  }
+  // PWHOLE: the scales and biases of all steps of the K range (local steps
+  // 0 .. steps-1) as one window per column and parameter of kPWholeBytes,
+  // from the dword that holds the range's first group: instruction i, lane L
+  // carries dword L%8 of column-parameter 8i + L/8 (scales of columns 0..63,
+  // then their biases) to LDS byte 256i + 4L of p_base (one buffer of
+  // 2 * 64 * kPWholeBytes).
+  __device__ __forceinline__ void issue_p_whole(int i) const {
+    const int cp = 8 * i + (lane >> 3);
+    const int64_t col = min(n0_ + (cp & 63), n_cols - 1);  // columns past N feed unstored outputs
+    const int off = 4 * min(window(s0) + (lane & 7), row_dwords - 1);
+    const uint8_t* src = cp < 64 ? s_whole + col * s_row_bytes : b_whole + col * b_row_bytes;
+    load_lds<4>(src + off, lds_address(p_base) + 256 * i);
   }
   __device__ __forceinline__ int w_buf(int step) const { return P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1); }
   __device__ __forceinline__ const uint8_t* w_lds(int step) const { return w_base + w_buf(step) * w_stride; }
@@ -277,6 +306,19 @@ struct WeightStream {
   // Raw scale and bias bits (bf16 in the low half, or f32) of local column c
   // for the group holding k offset `k` of `step`.
   __device__ __forceinline__ void params(int step, int c, int k, uint32_t* s_raw, uint32_t* b_raw) const {
+    if constexpr (PWHOLE) {
+      const int g = (((s0 + step) * kBK + k) >> (5 + group_shift)) - window(s0) * (4 / PT::bytes);
+      const uint8_t* sp = p_base + c * P::kPWholeBytes + PT::bytes * g;
+      const uint8_t* bp = sp + 64 * P::kPWholeBytes;
+      if constexpr (PT::bytes == 2) {
+        *s_raw = *reinterpret_cast<const uint16_t*>(sp);
+        *b_raw = *reinterpret_cast<const uint16_t*>(bp);
+      } else {
+        *s_raw = *reinterpret_cast<const uint32_t*>(sp);
+        *b_raw = *reinterpret_cast<const uint32_t*>(bp);
+      }
+      return;
+    }
     const int g = (((s0 + step) * kBK + k) >> (5 + group_shift)) - window(s0 + (step & ~3)) * (4 / PT::bytes);
     const uint8_t* pbuf = p_lds(step);
     if constexpr (PT::bytes == 2) {
