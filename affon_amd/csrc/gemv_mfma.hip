@@ -112,11 +112,15 @@ struct RowBlocks {
 // the prologue (issued before any other transfer, so every later wait covers
 // them), when they fit 32 bytes per column (e.g. 16 groups of bf16); this
 // cuts their memory requests by the number of 4-step windows.
-template <int BITS, typename PT, int XROWS, bool PWHOLE>
+//
+// WS: K steps per packed-word transfer (Plan): 8-bit words move two steps at
+// a time (whole 128-byte lines per column) where LDS has room for that ring
+// (up to 16 activation rows), one step at a time otherwise.
+template <int BITS, typename PT, int XROWS, bool PWHOLE, int WS = (BITS == 8 ? (XROWS <= 16 ? 2 : 1) : 4)>
 __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   TileArgs a = args;
   constexpr int kXLoads = XROWS / 8;  // activation DMA instructions per step
-  using P = Plan<BITS, PT, kXLoads, PWHOLE>;
+  using P = Plan<BITS, PT, kXLoads, PWHOLE, WS>;
   constexpr int RB = RowBlocks<XROWS>::kBlocks;
   constexpr int kRows = RowBlocks<XROWS>::kRows;
   __shared__ __attribute__((aligned(16))) uint8_t lds_x[kWaves][kStages][XROWS * 128];
@@ -173,7 +177,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     for (int i = 0; i < kXLoads; ++i)
       load_lds<16>(x_src[i] + (s0 + step) * kBK, lds_address(lds_x[wave][step & 3]) + 1024 * i);
   };
-  WeightStream<BITS, PT, kXLoads, PWHOLE> ws;
+  WeightStream<BITS, PT, kXLoads, PWHOLE, WS> ws;
   // PWHOLE keeps one window per wave: both window buffers of the wave, which
   // are adjacent when indexed [wave][buffer].
   uint8_t* p_base = PWHOLE ? lds_p[0][0] + wave * 2 * P::kPBytes : lds_p[0][wave];
@@ -181,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   auto issue_all = [&](int j, int pstep, int wstep, int astep) {
     if (j == 0 && !PWHOLE)
       for (int i = 0; i < P::kPLoads; ++i) ws.issue_p(pstep, i);
-    if (P::kStepsPerW == 1 || j == 0)
+    if (P::w_issue(j))
       for (int i = 0; i < P::kWLoads; ++i) ws.issue_w(wstep, i);
     issue_a(astep);
   };
@@ -217,15 +221,19 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) y[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Transfers exactly as the prefill GEMM orders them (Plan<..., kXLoads>),
-  // but each wave for itself: iterations -4 .. -1 issue the prologue,
-  // iteration t issues parameters and words at t%4 == 0 (2/4-bit) or every
-  // step (8-bit words), then the activations of step t+3. Step t is decoded
-  // in iteration t from LDS reads that complete before that iteration's
-  // transfers are issued: the 8-bit words of step t+4 reuse step t's buffer.
+  // Transfers in the order of the transfer plan (Plan<..., kXLoads, PWHOLE,
+  // WS>), each wave for itself: iterations -4 .. -1 issue the prologue,
+  // iteration t issues the parameter window at t%4 == 0 (unless PWHOLE),
+  // the words of steps t+4 .. t+7 at t%4 == 0 (four-step transfers), of step
+  // t+4 every step (one-step transfers) or of steps t+3, t+4 at odd t
+  // (two-step transfers), then the activations of step t+3. Step t is
+  // decoded in iteration t from LDS reads that complete before that
+  // iteration's transfers are issued, and the wait at its start covers
+  // exactly step t's transfers (Plan::wait_own): a transfer that reuses a
+  // buffer reuses the one of the step(s) just read.
 #define AFFON_QSKINNY_STEP(J)                                                                            \
   {                                                                                                      \
-    wait_vmcnt<P::wait(J)>();                                                                            \
+    wait_vmcnt<P::wait_own(J)>();                                                                        \
     bf16x8_t xf[RB][2];                                                                                  \
     _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                  \
       xf[rb][0] = read_x((J), rb, 0);                                                                    \
@@ -238,7 +246,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
       ws.params(t, 16 * ct + r, 0, &s_raw[ct], &b_raw[ct]);                                              \
     }                                                                                                    \
     wait_lds_reads();                                                                                    \
-    issue_all((J), min(t + 4, last & ~3), min(t + 4, P::kStepsPerW == 1 ? last : (last & ~3)),           \
+    issue_all((J), min(t + 4, last & ~3), min(t + P::kWAhead, last & ~(WS - 1)),                         \
               min(t + 3, last));                                                                         \
     f32x4_t xs[RB];                                                                                      \
     _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                  \
@@ -266,7 +274,8 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
       for (int i = 0; i < P::kPWholeLoads; ++i) ws.issue_p_whole(i);
     }
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) issue_all(rr, 0, min(rr, last), min(max(rr - 1, 0), last));
+    for (int rr = 0; rr < 4; ++rr)
+      issue_all(rr, 0, min(rr - 4 + P::kWAhead, last & ~(WS - 1)), min(max(rr - 1, 0), last));
     for (int t = 0; t < steps;) {
       AFFON_QSKINNY_STEP(0)
       AFFON_QSKINNY_STEP(1)

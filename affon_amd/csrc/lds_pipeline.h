@@ -145,10 +145,12 @@ struct Unroll<N, N> {
 // first step, instead of a window every four steps (WeightStream::
 // issue_p_whole; the caller checks that the range fits kPWholeBytes).
 //
-// Packed words reach LDS in runs of kColBytes per column: four K steps at a
-// time for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per column), one step at a
-// time for 8-bit (64 bytes) -- so each transfer instruction covers whole
-// half or full 128-byte lines. Inside a column run the 16-byte slots are
+// Packed words reach LDS in runs of kColBytes per column: WSTEPS K steps at
+// a time, by default four for 2/4-bit (64 / 128 bytes, 4 / 8 lanes per
+// column) and one for 8-bit (64 bytes) -- so each transfer instruction covers
+// whole half or full 128-byte lines. WSTEPS = 2 (8-bit: 128-byte runs, whole
+// lines) issues at odd iterations the two steps 3 and 4 ahead into a ring of
+// two buffers: the buffer written is the one of the two steps just read. Inside a column run the 16-byte slots are
 // XOR-swizzled with the column index so that the decode's fragment reads
 // (lanes = consecutive columns) are bank-conflict free whether the LDS serves
 // 8 lanes x 16 bytes (128 bytes) or 16 lanes x 16 bytes (256 bytes) per cycle. Scales and biases come as one 16-byte window per
@@ -156,9 +158,10 @@ struct Unroll<N, N> {
 // groups, f32: 4 groups), starting at the dword that holds the first group of
 // those 256 k values, which covers all of their groups for the group sizes
 // the kernel accepts; dwords past the row end repeat the row's last dword.
-template <int BITS, typename PT, int ALOADS, bool PWHOLE = false>
+template <int BITS, typename PT, int ALOADS, bool PWHOLE = false, int WSTEPS = (BITS == 8 ? 1 : 4)>
 struct Plan {
-  static constexpr int kStepsPerW = BITS == 8 ? 1 : 4;           // steps per packed-word transfer
+  static constexpr int kStepsPerW = WSTEPS;                       // steps per packed-word transfer
+  static_assert(WSTEPS == 1 || WSTEPS == 2 || WSTEPS == 4, "packed-word transfer length");
   static constexpr int kColBytes = 8 * BITS * kStepsPerW;         // bytes per column per transfer
   static constexpr int kSlots = kColBytes / 16;                   // 16-byte slots per column run
   static constexpr int kWLoads = 64 * kColBytes / 1024;           // 16-byte DMA instructions per transfer
@@ -180,10 +183,15 @@ struct Plan {
     return kSlots == 8 ? part ^ (c & 7) ^ ((c >> 3) & 1) : part ^ (((c >> 1) ^ (c >> 3)) & 3);
   }
 
+  // Whether iteration j issues a packed-word transfer, and how many steps
+  // ahead of the iteration's own step that transfer starts.
+  static constexpr bool w_issue(int j) { return kStepsPerW == 2 ? (j & 1) == 1 : (kStepsPerW == 1 || j == 0); }
+  static constexpr int kWAhead = kStepsPerW == 2 ? 3 : 4;
+
   // Transfers issued by iteration j (= step index mod 4), in issue order
   // parameters, words, activations; group 0 = parameters, 1 = words, 2 = activations.
   static constexpr int group_ops(int j, int g) {
-    return g == 0 ? (j == 0 && !PWHOLE ? kPLoads : 0) : g == 1 ? (kStepsPerW == 1 || j == 0 ? kWLoads : 0) : kALoads;
+    return g == 0 ? (j == 0 && !PWHOLE ? kPLoads : 0) : g == 1 ? (w_issue(j) ? kWLoads : 0) : kALoads;
   }
   static constexpr int ops(int j) { return group_ops(j, 0) + group_ops(j, 1) + group_ops(j, 2); }
   // Transfers issued after group g of the iteration r iterations before one
@@ -195,9 +203,25 @@ struct Plan {
     for (int i = 1; i < r; ++i) n += ops(((j - i) % 4 + 4) % 4);
     return n;
   }
+  // vmcnt bound at the start of iteration j when the iteration reads only
+  // its own step: the activations, words and parameters of that step must
+  // have landed (activations issued three iterations before; words by the
+  // transfer holding the step; parameters by the window holding it).
+  static constexpr int wait_own(int j) {
+    int n = ops_after(j, 3, 2);
+    const int rw = kStepsPerW == 1 ? 4 : kStepsPerW == 4 ? j + 4 : ((j & 1) ? 4 : 3);
+    const int nw = ops_after(j, rw, 1);
+    n = nw < n ? nw : n;
+    if (!PWHOLE) {
+      const int np = ops_after(j, j + 4, 0);
+      n = np < n ? np : n;
+    }
+    return n;
+  }
   // vmcnt bound at the start of iteration j: the activations of its step
   // (issued three iterations before) and the words and parameters of the
-  // next step (decoded during it) must have landed.
+  // next step (decoded during it) must have landed. (Transfers of one or
+  // four steps; the prefill GEMM's plan.)
   static constexpr int wait(int j) {
     int n = ops_after(j, 3, 2);
     const int rw = kStepsPerW == 1 ? 3 : (j == 3 ? 3 : j + 4);
@@ -215,9 +239,9 @@ struct Plan {
 // the wave's slices of a ring of LDS buffers: w_lds(buf) = w_base + buf *
 // w_stride (Plan::kWBufs buffers of kWBytes), p_lds(buf) likewise (2 buffers
 // of kPBytes). Steps passed to the methods are local to the K range.
-template <int BITS, typename PT, int ALOADS, bool PWHOLE = false>
+template <int BITS, typename PT, int ALOADS, bool PWHOLE = false, int WSTEPS = (BITS == 8 ? 1 : 4)>
 struct WeightStream {
-  using P = Plan<BITS, PT, ALOADS, PWHOLE>;
+  using P = Plan<BITS, PT, ALOADS, PWHOLE, WSTEPS>;
   const uint8_t* w_src[P::kWLoads];
   const uint8_t* s_col[4];
   const uint8_t* b_col[4];
@@ -283,7 +307,7 @@ struct WeightStream {
     const uint8_t* src = cp < 64 ? s_whole + col * s_row_bytes : b_whole + col * b_row_bytes;
     load_lds<4>(src + off, lds_address(p_base) + 256 * i);
   }
-  __device__ __forceinline__ int w_buf(int step) const { return P::kStepsPerW == 1 ? (step & 3) : ((step >> 2) & 1); }
+  __device__ __forceinline__ int w_buf(int step) const { return (step / P::kStepsPerW) % P::kWBufs; }
   __device__ __forceinline__ const uint8_t* w_lds(int step) const { return w_base + w_buf(step) * w_stride; }
   __device__ __forceinline__ const uint8_t* p_lds(int step) const { return p_base + ((step >> 2) & 1) * p_stride; }
   // Parameter window instruction i (0..3 scales, 4..7 biases) of the four
@@ -300,7 +324,7 @@ struct WeightStream {
   // Bytes [off, off + n) of local column c's packed run for `step`, as laid
   // out by the swizzle: 16-byte part q of the step's BITS*8 bytes.
   __device__ __forceinline__ const uint8_t* w_part(int step, int c, int q) const {
-    const int sub = P::kStepsPerW == 1 ? 0 : (step & 3);  // step within the transfer
+    const int sub = step % P::kStepsPerW;  // step within the transfer
     return w_lds(step) + c * P::kColBytes + 16 * P::slot(c, sub * (BITS / 2) + q);
   }
   // Raw scale and bias bits (bf16 in the low half, or f32) of local column c
