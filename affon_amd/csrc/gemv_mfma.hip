@@ -28,6 +28,10 @@ using namespace pipeline;
 constexpr int kMaxRows = 32;  // activation rows per tile: up to two blocks of 16 MFMA rows; more
                               // rows run as row tiles of 32 (grid dimension y)
 constexpr int kCols = 64;     // weight columns per workgroup (4 MFMA column tiles)
+// Each iteration of the decode-batch kernel issues its activation transfer
+// before its packed words (Plan, AFIRST), so the words stay in flight until
+// the step that needs them.
+constexpr bool kActsFirst = true;
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -120,7 +124,7 @@ template <int BITS, typename PT, int XROWS, bool PWHOLE, int WS = (BITS == 8 ? (
 __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   TileArgs a = args;
   constexpr int kXLoads = XROWS / 8;  // activation DMA instructions per step
-  using P = Plan<BITS, PT, kXLoads, PWHOLE, WS>;
+  using P = Plan<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst>;
   constexpr int RB = RowBlocks<XROWS>::kBlocks;
   constexpr int kRows = RowBlocks<XROWS>::kRows;
   __shared__ __attribute__((aligned(16))) uint8_t lds_x[kWaves][kStages][XROWS * 128];
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     for (int i = 0; i < kXLoads; ++i)
       load_lds<16>(x_src[i] + (s0 + step) * kBK, lds_address(lds_x[wave][step & 3]) + 1024 * i);
   };
-  WeightStream<BITS, PT, kXLoads, PWHOLE, WS> ws;
+  WeightStream<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst> ws;
   // PWHOLE keeps one window per wave: both window buffers of the wave, which
   // are adjacent when indexed [wave][buffer].
   uint8_t* p_base = PWHOLE ? lds_p[0][0] + wave * 2 * P::kPBytes : lds_p[0][wave];
@@ -185,9 +189,10 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   auto issue_all = [&](int j, int pstep, int wstep, int astep) {
     if (j == 0 && !PWHOLE)
       for (int i = 0; i < P::kPLoads; ++i) ws.issue_p(pstep, i);
+    if (kActsFirst) issue_a(astep);
     if (P::w_issue(j))
       for (int i = 0; i < P::kWLoads; ++i) ws.issue_w(wstep, i);
-    issue_a(astep);
+    if (!kActsFirst) issue_a(astep);
   };
   // A operand of MFMA t for row block rb: row 16rb + r (taken mod XROWS when
   // only 8 rows are staged), chunk 2h + t.

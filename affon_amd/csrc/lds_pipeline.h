@@ -150,7 +150,14 @@ struct Unroll<N, N> {
 // column) and one for 8-bit (64 bytes) -- so each transfer instruction covers
 // whole half or full 128-byte lines. WSTEPS = 2 (8-bit: 128-byte runs, whole
 // lines) issues at odd iterations the two steps 3 and 4 ahead into a ring of
-// two buffers: the buffer written is the one of the two steps just read. Inside a column run the 16-byte slots are
+// two buffers: the buffer written is the one of the two steps just read.
+//
+// Issue order within an iteration: parameters, words, activations; with
+// AFIRST parameters, activations, words. Transfers complete in issue order
+// for the load counter, so waiting for a step's activations (issued three
+// iterations before) also waits for every transfer issued before them:
+// with AFIRST the words issued in that same iteration stay in flight one
+// iteration longer. Inside a column run the 16-byte slots are
 // XOR-swizzled with the column index so that the decode's fragment reads
 // (lanes = consecutive columns) are bank-conflict free whether the LDS serves
 // 8 lanes x 16 bytes (128 bytes) or 16 lanes x 16 bytes (256 bytes) per cycle. Scales and biases come as one 16-byte window per
@@ -158,7 +165,8 @@ struct Unroll<N, N> {
 // groups, f32: 4 groups), starting at the dword that holds the first group of
 // those 256 k values, which covers all of their groups for the group sizes
 // the kernel accepts; dwords past the row end repeat the row's last dword.
-template <int BITS, typename PT, int ALOADS, bool PWHOLE = false, int WSTEPS = (BITS == 8 ? 1 : 4)>
+template <int BITS, typename PT, int ALOADS, bool PWHOLE = false, int WSTEPS = (BITS == 8 ? 1 : 4),
+          bool AFIRST = false>
 struct Plan {
   static constexpr int kStepsPerW = WSTEPS;                       // steps per packed-word transfer
   static_assert(WSTEPS == 1 || WSTEPS == 2 || WSTEPS == 4, "packed-word transfer length");
@@ -188,10 +196,16 @@ struct Plan {
   static constexpr bool w_issue(int j) { return kStepsPerW == 2 ? (j & 1) == 1 : (kStepsPerW == 1 || j == 0); }
   static constexpr int kWAhead = kStepsPerW == 2 ? 3 : 4;
 
-  // Transfers issued by iteration j (= step index mod 4), in issue order
-  // parameters, words, activations; group 0 = parameters, 1 = words, 2 = activations.
+  // Kinds of transfer and their position in an iteration's issue order.
+  static constexpr int kParams = 0, kWords = 1, kActs = 2;
+  static constexpr int pos(int kind) { return kind == kParams ? 0 : (kind == kWords) == !AFIRST ? 1 : 2; }
+  static constexpr int kind_ops(int j, int kind) {
+    return kind == kParams ? (j == 0 && !PWHOLE ? kPLoads : 0) : kind == kWords ? (w_issue(j) ? kWLoads : 0) : kALoads;
+  }
+  // Transfers issued by iteration j (= step index mod 4) in position g of
+  // its issue order.
   static constexpr int group_ops(int j, int g) {
-    return g == 0 ? (j == 0 && !PWHOLE ? kPLoads : 0) : g == 1 ? (w_issue(j) ? kWLoads : 0) : kALoads;
+    return g == 0 ? kind_ops(j, kParams) : kind_ops(j, g == pos(kWords) ? kWords : kActs);
   }
   static constexpr int ops(int j) { return group_ops(j, 0) + group_ops(j, 1) + group_ops(j, 2); }
   // Transfers issued after group g of the iteration r iterations before one
@@ -208,12 +222,12 @@ struct Plan {
   // have landed (activations issued three iterations before; words by the
   // transfer holding the step; parameters by the window holding it).
   static constexpr int wait_own(int j) {
-    int n = ops_after(j, 3, 2);
+    int n = ops_after(j, 3, pos(kActs));
     const int rw = kStepsPerW == 1 ? 4 : kStepsPerW == 4 ? j + 4 : ((j & 1) ? 4 : 3);
-    const int nw = ops_after(j, rw, 1);
+    const int nw = ops_after(j, rw, pos(kWords));
     n = nw < n ? nw : n;
     if (!PWHOLE) {
-      const int np = ops_after(j, j + 4, 0);
+      const int np = ops_after(j, j + 4, pos(kParams));
       n = np < n ? np : n;
     }
     return n;
@@ -223,10 +237,10 @@ struct Plan {
   // next step (decoded during it) must have landed. (Transfers of one or
   // four steps; the prefill GEMM's plan.)
   static constexpr int wait(int j) {
-    int n = ops_after(j, 3, 2);
+    int n = ops_after(j, 3, pos(kActs));
     const int rw = kStepsPerW == 1 ? 3 : (j == 3 ? 3 : j + 4);
     const int rp = j == 3 ? 3 : j + 4;
-    const int nw = ops_after(j, rw, 1), np = ops_after(j, rp, 0);
+    const int nw = ops_after(j, rw, pos(kWords)), np = ops_after(j, rp, pos(kParams));
     n = nw < n ? nw : n;
     if (!PWHOLE) n = np < n ? np : n;  // whole-range parameters precede every transfer waited for
     return n;
@@ -239,9 +253,10 @@ struct Plan {
 // the wave's slices of a ring of LDS buffers: w_lds(buf) = w_base + buf *
 // w_stride (Plan::kWBufs buffers of kWBytes), p_lds(buf) likewise (2 buffers
 // of kPBytes). Steps passed to the methods are local to the K range.
-template <int BITS, typename PT, int ALOADS, bool PWHOLE = false, int WSTEPS = (BITS == 8 ? 1 : 4)>
+template <int BITS, typename PT, int ALOADS, bool PWHOLE = false, int WSTEPS = (BITS == 8 ? 1 : 4),
+          bool AFIRST = false>
 struct WeightStream {
-  using P = Plan<BITS, PT, ALOADS, PWHOLE, WSTEPS>;
+  using P = Plan<BITS, PT, ALOADS, PWHOLE, WSTEPS, AFIRST>;
   const uint8_t* w_src[P::kWLoads];
   const uint8_t* s_col[4];
   const uint8_t* b_col[4];
