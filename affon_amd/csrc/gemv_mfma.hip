@@ -28,6 +28,7 @@ using namespace pipeline;
 constexpr int kMaxRows = 32;  // activation rows per tile: up to two blocks of 16 MFMA rows; more
                               // rows run as row tiles of 32 (grid dimension y)
 constexpr int kCols = 64;     // weight columns per workgroup (4 MFMA column tiles)
+constexpr int kReMinRows = 128;  // from here on the reassociated GEMM (gemm_re.hip) takes the problem
 // Each iteration of the decode-batch kernel issues its activation transfer
 // before its packed words (Plan, AFIRST), so the words stay in flight until
 // the step that needs them.
@@ -417,6 +418,12 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
       }
     default:
       break;
+  }
+  // Tall activations: the large-tile reassociated GEMM, when its scratch
+  // (per-group activation sums) can be had.
+  if (p.M >= kReMinRows && re_gemm_supports(p)) {
+    hipError_t e = hipSuccess;
+    if (re_gemm_launch(p, l, &e)) return e;
   }
   return tiled_launch(p, nullptr, 0, l);
 }

@@ -103,6 +103,14 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l);
 bool gemv_mfma_group_supports(const QmmProblem* group, int count);
 hipError_t gemv_mfma_group_launch(const QmmProblem* group, int count, const Launch& l);
 
+// The reassociated prefill GEMM (gemm_re.hip) that gemv_mfma_launch runs for
+// tall activations: 4-bit codes as exact bf16 MFMA operands, each group's
+// scale applied in f32, the bias term from per-group activation sums.
+bool re_gemm_supports(const QmmProblem& p);
+// Enqueues it and returns true (*status: the launch status), or returns
+// false with nothing enqueued when its scratch memory cannot be had now.
+bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status);
+
 bool mfma_supports(const QmmProblem& p);
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l);
 // The 4-bit prefill kernel whose column-sharing waves split the decode

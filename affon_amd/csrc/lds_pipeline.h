@@ -248,6 +248,23 @@ struct Plan {
   static_assert(kWLoads * 1024 == kWBytes, "whole DMA instructions");
 };
 
+// Transfer plan of the reassociated prefill GEMM (gemm_re.hip), per wave of
+// its eight: kSOps 4-byte scale transfers once (the tile's scales for the
+// whole K range), then iteration t issues kAOps activation transfers (step
+// t+2) and, when t % 4 == 0, kWOps packed-word transfers (steps t+4 .. t+7),
+// in that order. The prologue issues the scales, the packed words of steps
+// 0..3 and the activations of steps 0 and 1.
+struct RePlan {
+  static constexpr int kWaves = 8;
+  static constexpr int kAOps = 4, kWOps = 2, kSOps = 8;
+  // vmcnt bound at the start of iteration t (j = t % 4): the activations of
+  // step t (issued by iteration t-2, before its packed words) must have
+  // landed, which also covers step t's packed words and the scales (issued
+  // earlier). In flight may stay the packed words issued by iteration t-2
+  // (when t-2 = 0 mod 4) and every transfer of iteration t-1.
+  static constexpr int wait(int j) { return kAOps + (j == 1 || j == 2 ? kWOps : 0); }
+};
+
 // The packed-word and parameter transfers of one wave's 64 columns
 // [n0, n0 + 64) over one K range starting at global step s0, per Plan, into
 // the wave's slices of a ring of LDS buffers: w_lds(buf) = w_base + buf *
