@@ -103,29 +103,6 @@ __device__ __forceinline__ void decode_word(uint32_t w, float s, float b, u32x4_
   decode_piece<6>(w, s, b, d, out);
 }
 
-// 64-bit scalar pointer plus a byte offset, as an SGPR pair for the asm.
-__device__ __forceinline__ const uint8_t* sadd(const void* p, int64_t off) {
-  return static_cast<const uint8_t*>(p) + off;
-}
-
-// 16 bytes per lane from saddr + voff into LDS at lds_addr + 16 * lane.
-__device__ __forceinline__ void dma16(const uint8_t* saddr, uint32_t voff, uint32_t lds_addr) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(saddr), "s"(lds_addr)
-               : "memory", "m0");
-#pragma clang diagnostic pop
-}
-
-// 4 bytes per lane from saddr + voff into LDS at lds_addr + 4 * lane.
-__device__ __forceinline__ void dma4(const uint8_t* saddr, uint32_t voff, uint32_t lds_addr) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(saddr), "s"(lds_addr)
-               : "memory", "m0");
-#pragma clang diagnostic pop
-}
-
 template <typename PT, int MI>
 __device__ __forceinline__ void pair_tile(const TileArgs& a, uint8_t* lds_a, uint8_t* lds_bx, uint8_t* lds_w,
                                           uint8_t* lds_p, int m0, int n0, int split) {

@@ -59,8 +59,7 @@ static_assert(kCols * kSCol / 256 / kReWaves == RePlan::kSOps, "scale transfers 
 
 struct ReArgs {
   TileArgs t;
-  const uint16_t* planes;  // [3][M][gp] bf16: X1, X2, X3 of every row and group
-  int gp;                  // plane row stride (groups, a multiple of 8)
+  const uint16_t* planes;  // [K range][3][M][kMaxGroups] bf16: X1, X2, X3 of every row and group
 };
 
 // Slot (16-byte unit) of part `part` (0..7) in local column c's 128-byte
@@ -73,42 +72,30 @@ __device__ __forceinline__ int w_slot(int c, int part) { return part ^ (c & 7) ^
 // fragment reads (consecutive rows, one chunk) are bank-conflict free.
 __device__ __forceinline__ int a_slot(int r, int q) { return q ^ (r & 7) ^ ((r >> 3) & 1); }
 
-// B operand of MFMA kk from the lane's packed word kk (codes 8 per word, code
-// i in nibble i): the codes as exact bf16 integers times 2^-9 (a byte holding
-// n < 16 reads as n * 2^-9 in FP8 E4M3; the scale carries 2^9).
-__device__ __forceinline__ bf16x8_t codes_op(uint32_t w) {
-  const uint32_t even = w & 0x0f0f0f0fu;         // byte j = code 2j
-  const uint32_t odd = (w >> 4) & 0x0f0f0f0fu;   // byte j = code 2j+1
-  const uint32_t lo = __builtin_amdgcn_perm(odd, even, 0x05010400u);  // codes 0,1,2,3
-  const uint32_t hi = __builtin_amdgcn_perm(odd, even, 0x07030602u);  // codes 4,5,6,7
-  const u32x4_t v{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false)),
-                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true)),
-                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false)),
-                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true))};
-  return __builtin_bit_cast(bf16x8_t, v);
-}
-
-// X = sum of the `group` activations of one row and group in f32 (k order),
-// stored as three bf16 planes whose sum is X exactly; plane entries past the
-// last group are zero.
-__global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* x, int64_t xs0, int M, int G, int gp,
-                                                         int group, uint16_t* planes) {
+// X = sum of the `group` activations of one row and group in f32, stored as
+// three bf16 planes whose sum is X exactly. Layout [range][plane][row][64]:
+// group g of K range g / range_groups at entry g % range_groups of a 128-byte
+// row (entries past the range's groups are never used unmasked). Thread i
+// reads 16-byte chunk i of the activations (row i / (K/8)); the group/8
+// consecutive lanes of one group add their partial sums by lane exchange and
+// the first stores.
+__global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* x, int64_t xs0, int M, int K, int group,
+                                                         int range_groups, uint16_t* planes) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= static_cast<int64_t>(M) * gp) return;
-  const int row = static_cast<int>(i / gp);
-  const int g = static_cast<int>(i % gp);
+  const int chunks = K / 8;
+  if (i >= static_cast<int64_t>(M) * chunks) return;  // whole groups of lanes (chunks % 32 == 0)
+  const int row = static_cast<int>(i / chunks);
+  const int c = static_cast<int>(i % chunks);
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(x + row * xs0 + 8 * c);
   float sum = 0.0f;
-  if (g < G) {
-    const uint16_t* p = x + row * xs0 + static_cast<int64_t>(g) * group;
-    for (int k = 0; k < group; k += 8) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p + k);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sum += __uint_as_float(v[e] << 16);
-        sum += __uint_as_float(v[e] & 0xffff0000u);
-      }
-    }
+  for (int e = 0; e < 4; ++e) {
+    sum += __uint_as_float(v[e] << 16);
+    sum += __uint_as_float(v[e] & 0xffff0000u);
   }
+  const int lanes = group / 8;
+  for (int o = 1; o < lanes; o <<= 1) sum += __shfl_xor(sum, o);
+  if (c % lanes != 0) return;
   const uint16_t h1 = f32_to_bf16_bits(sum);
   uint16_t h2 = 0, h3 = 0;
   if (__builtin_isfinite(sum)) {
@@ -116,12 +103,51 @@ __global__ __launch_bounds__(256) void group_sums_kernel(const uint16_t* x, int6
     h2 = f32_to_bf16_bits(r1);
     h3 = f32_to_bf16_bits(r1 - bf16_bits_to_f32(h2));  // exact: the remaining bits fit bf16
   }
-  planes[i] = h1;
-  planes[static_cast<int64_t>(M) * gp + i] = h2;
-  planes[2 * static_cast<int64_t>(M) * gp + i] = h3;
+  const int g = c / lanes;
+  const int64_t plane = static_cast<int64_t>(M) * kMaxGroups;
+  const int64_t at = (g / range_groups) * 3 * plane + static_cast<int64_t>(row) * kMaxGroups + g % range_groups;
+  planes[at] = h1;
+  planes[plane + at] = h2;
+  planes[2 * plane + at] = h3;
+}
+
+// Decode of one packed word into an MFMA B operand in two pieces, so that a
+// step's decode can be spread over its MFMAs: piece 0 separates and orders
+// the nibbles (codes 0..3 and 4..7, one per byte), piece 1 converts them. A
+// byte holding n < 16 reads as n * 2^-9 in FP8 E4M3; the conversion's scale
+// 2^9 makes the operand the exact integer codes.
+struct CodePair {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ CodePair codes_split(uint32_t w) {
+  const uint32_t even = w & 0x0f0f0f0fu;        // byte j = code 2j
+  const uint32_t odd = (w >> 4) & 0x0f0f0f0fu;  // byte j = code 2j+1
+  return CodePair{__builtin_amdgcn_perm(odd, even, 0x05010400u),   // codes 0,1,2,3
+                  __builtin_amdgcn_perm(odd, even, 0x07030602u)};  // codes 4,5,6,7
+}
+__device__ __forceinline__ bf16x8_t codes_convert(CodePair p) {
+  const u32x4_t v{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(p.lo, 512.0f, false)),
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(p.lo, 512.0f, true)),
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(p.hi, 512.0f, false)),
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(p.hi, 512.0f, true))};
+  return __builtin_bit_cast(bf16x8_t, v);
 }
 
 // GSTEPS: K steps per group (1: group 64, 2: group 128).
+//
+// Accumulator tiles of a wave: T = mt + 2*nt (rows 32*mt.., columns 32*nt..
+// of the wave's 64 x 64). One step is 16 slots, each one MFMA plus about
+// eight vector instructions, in this order (the scheduling barriers keep it):
+//   slots 0..7   MFMAs of tiles 0, 1 (chunk kk = slot/2), B operands of
+//                column block 0 (decoded during the previous step); beside
+//                them the scaling of tiles 2, 3 of the previous step and the
+//                decode of column block 1 of this step;
+//   slots 8..15  MFMAs of tiles 2, 3; beside them the scaling of tiles 0, 1
+//                and the decode of column block 0 of the next step.
+// A tile is scaled (y += s * group sums) at least two slots after its last
+// MFMA and before its next first one, so one set of group-sum accumulators
+// suffices and the matrix core and the vector ALU work side by side within
+// a wave.
 template <int GSTEPS>
 __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   const TileArgs& a = r.t;
@@ -152,34 +178,35 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   // Activation transfers: this wave fills 8-row groups g8 = kAOps*wave + i of
   // a stage; lane L writes slot L%8 of local row 8*g8 + L/8, so it loads chunk
   // (L%8) ^ (L/8) ^ (g8%2). Rows past M repeat row M-1 (unstored outputs).
-  const uint16_t* a_src[RePlan::kAOps];
+  // Lane offsets are 32-bit from the step's scalar base x + 128*(s0+step).
+  uint32_t a_off[RePlan::kAOps];
 #pragma unroll
   for (int i = 0; i < RePlan::kAOps; ++i) {
     const int g8 = RePlan::kAOps * wave + i;
     const int row = min(m0 + 8 * g8 + (lane >> 3), a.M - 1);
-    a_src[i] = a.x + static_cast<int64_t>(row) * a.xs0 + 8 * ((lane & 7) ^ (lane >> 3) ^ (g8 & 1));
+    a_off[i] = static_cast<uint32_t>(row * a.xs0 * 2) + 16 * ((lane & 7) ^ (lane >> 3) ^ (g8 & 1));
   }
   auto issue_a = [&](int step, int stage) {
+    const uint8_t* base = sadd(a.x, static_cast<int64_t>(s0 + step) * 128);
 #pragma unroll
     for (int i = 0; i < RePlan::kAOps; ++i)
-      load_lds<16>(a_src[i] + static_cast<int64_t>(s0 + step) * kBK,
-                   lds_address(lds_a[0]) + stage * kAStage + 1024 * (RePlan::kAOps * wave + i));
+      dma16(base, a_off[i], lds_address(lds_a[0]) + stage * kAStage + 1024 * (RePlan::kAOps * wave + i));
   };
   // Packed-word transfers: instruction j = kWOps*wave + i, lane L writes byte
   // 1024j + 16L of a buffer = physical slot L%8 of local column 8j + L/8.
-  const uint8_t* w_src[RePlan::kWOps];
+  uint32_t w_off[RePlan::kWOps];
 #pragma unroll
   for (int i = 0; i < RePlan::kWOps; ++i) {
     const int c = 8 * (RePlan::kWOps * wave + i) + (lane >> 3);
     const int col = min(n0 + c, a.N - 1);  // columns past N feed unstored outputs
-    w_src[i] = reinterpret_cast<const uint8_t*>(a.w + static_cast<int64_t>(col) * a.ws0) + 16 * w_slot(c, lane & 7);
+    w_off[i] = static_cast<uint32_t>(col * a.ws0 * 4) + 16 * w_slot(c, lane & 7);
   }
   // The packed words of steps step4 .. step4+3 into buffer buf.
   auto issue_w = [&](int step4, int buf) {
+    const uint8_t* base = sadd(a.w, static_cast<int64_t>(s0 + step4) * 32);
 #pragma unroll
     for (int i = 0; i < RePlan::kWOps; ++i)
-      load_lds<16>(w_src[i] + static_cast<int64_t>(s0 + step4) * 32,
-                   lds_address(lds_w[0]) + buf * kWBuf + 1024 * (RePlan::kWOps * wave + i));
+      dma16(base, w_off[i], lds_address(lds_w[0]) + buf * kWBuf + 1024 * (RePlan::kWOps * wave + i));
   };
   // Scales of the K range: column c holds 32 dwords (groups g0 .. g0+63),
   // dword d at physical dword d ^ (c%32), so the per-step reads (32
@@ -194,42 +221,66 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
     const int d = min((g0 >> 1) + ((lane & 31) ^ (c & 31)), row_dwords - 1);
     load_lds<4>(a.s + static_cast<int64_t>(col) * a.ss0 * 2 + 4 * d, lds_address(lds_s) + 256 * i);
   };
-  // Scale (times 2^9) of local column c for global group g of the range.
-  auto scale = [&](int c, int g) -> float {
+  // Scale of column block nt (local column 64*ni + 32*nt + li) for global
+  // group g of the range.
+  const int s_lane = kSCol * (64 * ni + li);
+  auto scale = [&](int nt, int g) -> float {
     const int gl = g - g0;
-    const int d = (gl >> 1) ^ (c & 31);
-    const uint32_t bits = *reinterpret_cast<const uint16_t*>(lds_s + kSCol * c + 4 * d + 2 * (gl & 1));
-    return bf16_bits_to_f32(bits) * 512.0f;
+    const uint32_t bits = *reinterpret_cast<const uint16_t*>(lds_s + s_lane + kSCol * 32 * nt + 4 * ((gl >> 1) ^ li) +
+                                                              2 * (gl & 1));
+    return bf16_bits_to_f32(bits);
   };
-  // A fragment (mt, kk): local row 64*mi + 32*mt + li, chunk 4*lh + kk.
+  // A fragment (mt, kk): local row 64*mi + 32*mt + li, chunk 4*lh + kk. The
+  // swizzle depends on the row only through li, so mt adds 4096 bytes.
+  int a_rd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int row = 64 * mi + li;
+    a_rd[kk] = (row >> 3) * 1024 + (8 * (row & 7) + a_slot(row, 4 * lh + kk)) * 16;
+  }
   auto read_a = [&](int stage, int mt, int kk) -> bf16x8_t {
-    const int row = 64 * mi + 32 * mt + li;
-    return *reinterpret_cast<const bf16x8_t*>(&lds_a[0][0] + stage * kAStage + (row >> 3) * 1024 +
-                                              (8 * (row & 7) + a_slot(row, 4 * lh + kk)) * 16);
+    return *reinterpret_cast<const bf16x8_t*>(&lds_a[0][0] + stage * kAStage + a_rd[kk] + 4096 * mt);
   };
-  // The lane's four packed words of column 64*ni + 32*nt + li for step t.
-  auto read_w = [&](int t, int nt) -> u32x4_t {
-    const int c = 64 * ni + 32 * nt + li;
-    return *reinterpret_cast<const u32x4_t*>(&lds_w[0][0] + ((t >> 2) & 1) * kWBuf + kWRun * c +
-                                             16 * w_slot(c, 2 * (t & 3) + lh));
+  // The lane's four packed words of column block nt for a step with t % 4 =
+  // sub in buffer buf: local column 64*ni + 32*nt + li (nt adds 32 columns,
+  // the same swizzle), part 2*sub + lh.
+  int w_rd[4];
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) {
+    const int c = 64 * ni + li;
+    w_rd[sub] = kWRun * c + 16 * w_slot(c, 2 * sub + lh);
+  }
+  auto read_w = [&](int buf, int sub, int nt) -> u32x4_t {
+    return *reinterpret_cast<const u32x4_t*>(&lds_w[0][0] + buf * kWBuf + w_rd[sub] + kWRun * 32 * nt);
   };
 
   // Prologue, as the issue order the waits count (RePlan): scales; packed
-  // words of steps 0..3; activations of steps 0 and 1.
+  // words of steps 0..3; activations of steps 0 and 1. Then the B operands of
+  // column block 0 for step 0 (the loop decodes them one step ahead).
 #pragma unroll
   for (int ii = 0; ii < RePlan::kSOps; ++ii) issue_s(ii);
   issue_w(0, 0);
   issue_a(0, 0);
   issue_a(min(1, last), 1);
+  wait_vmcnt<2 * RePlan::kAOps>();  // the scales and the packed words of steps 0..3
+  __syncthreads();
+  bf16x8_t bq0[4], bq1[4];  // B operands of column blocks 0 and 1, by chunk
+  {
+    const u32x4_t w = read_w(0, 0, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) bq0[kk] = codes_convert(codes_split(w[kk]));
+  }
 
-  f32x16_t y[2][2], acc[2][2];
+  f32x16_t y[4], acc[4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int T = 0; T < 4; ++T)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) y[mt][nt][v] = 0.0f;
+    for (int v = 0; v < 16; ++v) {
+      y[T][v] = 0.0f;
+      acc[T][v] = 0.0f;  // tiles 2, 3 of "step -1" are scaled by 0 in the first step
+    }
   const f32x16_t zero = {};
+  float sc_prev1 = 0.0f;  // scale of column block 1 for the previous step
 
   int stage = 0;  // t % 3
   for (int t = 0; t < steps; t += 4) {
@@ -246,67 +297,132 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
       issue_a(min(tt + 2, last), stage == 0 ? 2 : stage - 1);
       if constexpr (J == 0) issue_w(min(tt + 4, last & ~3), ((tt >> 2) + 1) & 1);
 
-      const u32x4_t wv[2] = {read_w(tt, 0), read_w(tt, 1)};
-      constexpr bool kFirst = GSTEPS == 1 || (J & 1) == 0;  // first step of its group
-      constexpr bool kLast = GSTEPS == 1 || (J & 1) == 1;   // last step of its group
+      // LDS reads two slots before their first use, so that they do not all
+      // queue behind each other at the start of the step: the fragments of
+      // chunk 0 and the packed words of column block 1 first; then in slot s
+      // < 6 the fragment slot s+2 takes; in slot 6 the packed words of column
+      // block 0 for the next step (the last step reads its own again) and the
+      // step's scales.
+      bf16x8_t af[2][4];
+      af[0][0] = read_a(stage, 0, 0);
+      af[1][0] = read_a(stage, 1, 0);
+      const int buf = (tt >> 2) & 1;
+      const u32x4_t wv1 = read_w(buf, J, 1);
+      u32x4_t wv0;
+      float sc0, sc1;
+      constexpr bool kFirst = GSTEPS == 1 || (J & 1) == 0;     // first step of its group
+      constexpr bool kLast = GSTEPS == 1 || (J & 1) == 1;      // last step of its group
+      constexpr bool kPrevLast = GSTEPS == 1 || (J & 1) == 0;  // the previous step ended a group
+      CodePair cp;
+      Unroll<0, 16>::run([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        constexpr int half = s / 8, rr = s % 8, kk = rr / 2, mt = rr % 2, nt = half, T = mt + 2 * nt;
+        if constexpr (s < 6) {
+          af[s % 2][s / 2 + 1] = read_a(stage, s % 2, s / 2 + 1);
+        } else if constexpr (s == 6) {
+          wv0 = J == 3 ? read_w(tt + 1 <= last ? buf ^ 1 : buf, tt + 1 <= last ? 0 : 3, 0) : read_w(buf, J + 1, 0);
+          const int g = (s0 + tt) / GSTEPS;
+          sc0 = scale(0, g);
+          sc1 = scale(1, g);
+        }
+        acc[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt][kk], nt == 0 ? bq0[kk] : bq1[kk],
+                                                         (kFirst && kk == 0) ? zero : acc[T], 0, 0, 0);
+        // Scaling: four elements of tile 2 + rr/4 (previous step) or rr/4.
+        constexpr int ST = half == 0 ? 2 + rr / 4 : rr / 4, v0 = 4 * (rr % 4);
+        if constexpr (half == 0 ? kPrevLast : kLast) {
+          const float s_t = half == 0 ? sc_prev1 : sc0;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8_t af[2] = {read_a(stage, 0, kk), read_a(stage, 1, kk)};
-        const bf16x8_t bq[2] = {codes_op(wv[0][kk]), codes_op(wv[1][kk])};
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bq[nt],
-                                                                  (kFirst && kk == 0) ? zero : acc[mt][nt], 0, 0, 0);
-      }
-      if constexpr (kLast) {
-        const int g = (s0 + tt) / GSTEPS;
-        const float sc[2] = {scale(64 * ni + li, g), scale(64 * ni + 32 + li, g)};
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) y[mt][nt][v] = fmaf(sc[nt], acc[mt][nt][v], y[mt][nt][v]);
-      }
+          for (int v = v0; v < v0 + 4; ++v) y[ST][v] = fmaf(s_t, acc[ST][v], y[ST][v]);
+        }
+        // Decode: word rr/2 of column block 1 (this step) or 0 (next step).
+        const uint32_t word = (half == 0 ? wv1 : wv0)[rr / 2];
+        if constexpr (rr % 2 == 0) {
+          cp = codes_split(word);
+        } else if constexpr (half == 0) {
+          bq1[rr / 2] = codes_convert(cp);
+        } else {
+          bq0[rr / 2] = codes_convert(cp);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      sc_prev1 = sc1;
       stage = stage == 2 ? 0 : stage + 1;
     });
   }
-  // Leave no transfer in flight (the last iterations re-fetch the final step).
-  wait_vmcnt<0>();
-
   // Bias term: y += sum over the range's groups of X_t[row][g] * b[col][g],
-  // 16 groups per MFMA; lane half h takes groups gb .. gb+7, gb = c0 + 8h.
-  // Groups past the range end enter as zeros on both sides.
-  for (int c0 = g0; c0 < g1; c0 += 16) {
-    const int gb = c0 + 8 * lh;
-    u32x4_t bb[2];
+  // 16 groups per MFMA. Its operands go through LDS, brought by whole-line
+  // transfers once every wave is done with the loop's buffers: the tile's
+  // rows of the three planes (this range's 128-byte rows, groups g0 ..
+  // g0+63) into the activation ring, plane t at 32 KiB * t, row r at 128 * r,
+  // 16-byte slot q at a_slot(r, q); the tile's biases into the scale area
+  // with the scales' layout.
+  wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
+  __syncthreads();
+  {
+    static_assert(3 * kRows * 128 <= kAStages * kAStage, "three plane tiles fit the activation ring");
+    static_assert(3 * kRows / 8 % kReWaves == 0, "whole plane transfers per wave");
+    constexpr int kXOps = 3 * kRows / 8 / kReWaves;
+    const uint16_t* planes = r.planes + static_cast<int64_t>(split) * 3 * a.M * kMaxGroups;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = min(n0 + 64 * ni + 32 * nt + li, a.N - 1);
-      const uint32_t* bp = reinterpret_cast<const uint32_t*>(a.b + (static_cast<int64_t>(col) * a.bs0 + gb) * 2);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bb[nt][e] = gb + 2 * e < g1 ? bp[e] : 0u;
+    for (int ii = 0; ii < kXOps; ++ii) {
+      const int i = kXOps * wave + ii;  // plane i / 32, rows 8*(i%32) ..
+      const int pl = i / (kRows / 8), rg = i % (kRows / 8);
+      const int row = min(m0 + 8 * rg + (lane >> 3), a.M - 1);
+      const int q = (lane & 7) ^ (lane >> 3) ^ (rg & 1);
+      load_lds<16>(planes + (static_cast<int64_t>(pl) * a.M + row) * kMaxGroups + 8 * q,
+                   lds_address(lds_a[0]) + pl * (kRows * 128) + 1024 * rg);
     }
+    const int row_dwords = (a.K >> (5 + a.group_shift)) / 2;
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl) {
-      u32x4_t xv[2];
+    for (int ii = 0; ii < RePlan::kSOps; ++ii) {
+      const int i = RePlan::kSOps * wave + ii;
+      const int c = 2 * i + (lane >> 5);
+      const int col = min(n0 + c, a.N - 1);
+      const int d = min((g0 >> 1) + ((lane & 31) ^ (c & 31)), row_dwords - 1);
+      load_lds<4>(a.b + static_cast<int64_t>(col) * a.bs0 * 2 + 4 * d, lds_address(lds_s) + 256 * i);
+    }
+  }
+  // Tiles 2, 3 of the last step (the range ends a group), while the transfers fly.
+#pragma unroll
+  for (int T = 2; T < 4; ++T)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc_prev1, acc[T][v], y[T][v]);
+  wait_vmcnt<0>();
+  __syncthreads();
+  // Chunk c: lane half h takes local groups 16c + 8h .. +7; entries of groups
+  // past the range are replaced by zeros on both sides.
+  const int gcount = g1 - g0;
+#pragma unroll
+  for (int c = 0; c < kMaxGroups / 16; ++c) {
+    const int gl = 16 * c + 8 * lh;
+    u32x4_t bb[2], xv[3][2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(lds_s + s_lane + kSCol * 32 * nt +
+                                                             4 * (((gl >> 1) + e) ^ li));
+        bb[nt][e] = gl + 2 * e < gcount ? v : 0u;
+      }
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const int row = min(m0 + 64 * mi + 32 * mt + li, a.M - 1);
-        const uint32_t* xp =
-            reinterpret_cast<const uint32_t*>(r.planes + (static_cast<int64_t>(pl) * a.M + row) * r.gp + gb);
+        const int row = 64 * mi + 32 * mt + li;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds_a[0][0] + pl * (kRows * 128) + row * 128 +
+                                                            16 * a_slot(row, 2 * c + lh));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xv[mt][e] = gb + 2 * e < g1 ? xp[e] : 0u;
+        for (int e = 0; e < 4; ++e) xv[pl][mt][e] = gl + 2 * e < gcount ? v[e] : 0u;
       }
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
-          y[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[mt]),
-                                                              __builtin_bit_cast(bf16x8_t, bb[nt]), y[mt][nt], 0, 0, 0);
-    }
+          y[mt + 2 * nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][mt]),
+                                                                   __builtin_bit_cast(bf16x8_t, bb[nt]),
+                                                                   y[mt + 2 * nt], 0, 0, 0);
   }
 
   // Accumulator (mt, nt) element v of lane l is row 8*(v/4) + 4*(l/32) + v%4
@@ -329,7 +445,7 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
             if (full || m0 + rr < a.M) {
               const uint32_t off = static_cast<uint32_t>(rr * a.N + col) * 4u;
               store_as<KIND>(a.epi, reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(base) + off), col,
-                             y[mt][nt][v]);
+                             y[mt + 2 * nt][v]);
             }
           }
       }
@@ -371,10 +487,9 @@ bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status) {
   const int tiles = ((N + kCols - 1) / kCols) * ((M + kRows - 1) / kRows);
   const int splits = re_splits(tiles, steps, gsteps);
   if (splits == 0) return false;
-  const int G = static_cast<int>(K / p.group);
-  const int gp = (G + 7) & ~7;
+  const int range_groups = steps / splits / gsteps;
   const size_t partial_bytes = splits > 1 ? static_cast<size_t>(splits) * M * N * 4 : 0;
-  const size_t plane_bytes = static_cast<size_t>(3) * M * gp * 2;
+  const size_t plane_bytes = static_cast<size_t>(splits) * 3 * M * kMaxGroups * 2;
   const size_t total = ((partial_bytes + 255) & ~size_t(255)) + plane_bytes;
   if (l.fixed != nullptr && total > l.fixed_bytes) return false;  // the caller's other path runs instead
   uint8_t* scratch = static_cast<uint8_t*>(l.scratch(total));
@@ -400,11 +515,10 @@ bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status) {
   a.split_steps = steps / splits;
   a.partial = splits > 1 ? reinterpret_cast<float*>(scratch) : nullptr;
   r.planes = reinterpret_cast<const uint16_t*>(scratch + ((partial_bytes + 255) & ~size_t(255)));
-  r.gp = gp;
 
-  const int64_t sums = static_cast<int64_t>(M) * gp;
-  hipLaunchKernelGGL(group_sums_kernel, dim3(static_cast<unsigned>((sums + 255) / 256)), dim3(256), 0, l.stream,
-                     a.x, a.xs0, M, G, gp, static_cast<int>(p.group), const_cast<uint16_t*>(r.planes));
+  const int64_t chunks = static_cast<int64_t>(M) * (K / 8);
+  hipLaunchKernelGGL(group_sums_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, l.stream,
+                     a.x, a.xs0, M, K, static_cast<int>(p.group), range_groups, const_cast<uint16_t*>(r.planes));
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
     if (gsteps == 1)

@@ -120,6 +120,32 @@ __device__ __forceinline__ void load_lds(const void* src, uint32_t lds_addr) {
 #pragma clang diagnostic pop
 }
 
+// 64-bit scalar pointer plus a byte offset, as an SGPR pair for the asm.
+__device__ __forceinline__ const uint8_t* sadd(const void* p, int64_t off) {
+  return static_cast<const uint8_t*>(p) + off;
+}
+
+// The transfers of load_lds with a scalar (wave-uniform) base address saddr
+// and a 32-bit per-lane offset voff, so that per-step address advances stay
+// scalar work. 16 bytes per lane from saddr + voff into LDS at
+// lds_addr + 16 * lane.
+__device__ __forceinline__ void dma16(const uint8_t* saddr, uint32_t voff, uint32_t lds_addr) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(saddr), "s"(lds_addr)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// 4 bytes per lane from saddr + voff into LDS at lds_addr + 4 * lane.
+__device__ __forceinline__ void dma4(const uint8_t* saddr, uint32_t voff, uint32_t lds_addr) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(saddr), "s"(lds_addr)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
