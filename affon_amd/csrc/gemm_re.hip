@@ -135,19 +135,20 @@ __device__ __forceinline__ bf16x8_t codes_convert(CodePair p) {
 
 // GSTEPS: K steps per group (1: group 64, 2: group 128).
 //
-// Accumulator tiles of a wave: T = mt + 2*nt (rows 32*mt.., columns 32*nt..
-// of the wave's 64 x 64). One step is 16 slots, each one MFMA plus about
-// eight vector instructions, in this order (the scheduling barriers keep it):
-//   slots 0..7   MFMAs of tiles 0, 1 (chunk kk = slot/2), B operands of
-//                column block 0 (decoded during the previous step); beside
-//                them the scaling of tiles 2, 3 of the previous step and the
-//                decode of column block 1 of this step;
-//   slots 8..15  MFMAs of tiles 2, 3; beside them the scaling of tiles 0, 1
-//                and the decode of column block 0 of the next step.
-// A tile is scaled (y += s * group sums) at least two slots after its last
-// MFMA and before its next first one, so one set of group-sum accumulators
-// suffices and the matrix core and the vector ALU work side by side within
-// a wave.
+// Waves: 2 (rows) x 4 (columns); wave (mi, ni) computes rows 128*mi .. +127
+// and columns 32*ni .. +31 of the tile as accumulator tiles T = 0..3 (rows
+// 32*T .. of its 128), all four on the same B operands, so a wave decodes
+// only its 32 columns. One step is 16 slots, each one MFMA plus about seven
+// vector instructions, in this order (the scheduling barriers keep it):
+//   slots 0..7   MFMAs of tiles 0, 1 (chunk kk = slot/2), beside them the
+//                scaling of tiles 2, 3 of the previous step;
+//   slots 8..15  MFMAs of tiles 2, 3, beside them the scaling of tiles 0, 1;
+// and through slots 2..13 the decode of the next step's B operands, three
+// slots per packed word. A tile is scaled (y += s * group sums) at least two
+// slots after its last MFMA and before its next first one, so one set of
+// group-sum accumulators suffices and the matrix core and the vector ALU
+// work side by side within a wave. Each A fragment feeds one MFMA and is read
+// from LDS three slots ahead of it.
 template <int GSTEPS>
 __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   const TileArgs& a = r.t;
@@ -160,8 +161,8 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   const int lane = tid & 63;
   const int li = lane & 31;
   const int lh = lane >> 5;
-  const int mi = wave >> 1;  // rows 64*mi ..
-  const int ni = wave & 1;   // columns 64*ni ..
+  const int mi = wave >> 2;  // rows 128*mi ..
+  const int ni = wave & 3;   // columns 32*ni ..
 
   const int nb_n = (a.N + kCols - 1) / kCols;
   int tile, split;
@@ -186,11 +187,14 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
     const int row = min(m0 + 8 * g8 + (lane >> 3), a.M - 1);
     a_off[i] = static_cast<uint32_t>(row * a.xs0 * 2) + 16 * ((lane & 7) ^ (lane >> 3) ^ (g8 & 1));
   }
+  // Activation transfer instruction i of step `step` into ring stage `stage`.
+  auto issue_a1 = [&](int step, int stage, int i) {
+    dma16(sadd(a.x, static_cast<int64_t>(s0 + step) * 128), a_off[i],
+          lds_address(lds_a[0]) + stage * kAStage + 1024 * (RePlan::kAOps * wave + i));
+  };
   auto issue_a = [&](int step, int stage) {
-    const uint8_t* base = sadd(a.x, static_cast<int64_t>(s0 + step) * 128);
 #pragma unroll
-    for (int i = 0; i < RePlan::kAOps; ++i)
-      dma16(base, a_off[i], lds_address(lds_a[0]) + stage * kAStage + 1024 * (RePlan::kAOps * wave + i));
+    for (int i = 0; i < RePlan::kAOps; ++i) issue_a1(step, stage, i);
   };
   // Packed-word transfers: instruction j = kWOps*wave + i, lane L writes byte
   // 1024j + 16L of a buffer = physical slot L%8 of local column 8j + L/8.
@@ -201,12 +205,14 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
     const int col = min(n0 + c, a.N - 1);  // columns past N feed unstored outputs
     w_off[i] = static_cast<uint32_t>(col * a.ws0 * 4) + 16 * w_slot(c, lane & 7);
   }
-  // The packed words of steps step4 .. step4+3 into buffer buf.
+  // Instruction i of the packed words of steps step4 .. step4+3 into buffer buf.
+  auto issue_w1 = [&](int step4, int buf, int i) {
+    dma16(sadd(a.w, static_cast<int64_t>(s0 + step4) * 32), w_off[i],
+          lds_address(lds_w[0]) + buf * kWBuf + 1024 * (RePlan::kWOps * wave + i));
+  };
   auto issue_w = [&](int step4, int buf) {
-    const uint8_t* base = sadd(a.w, static_cast<int64_t>(s0 + step4) * 32);
 #pragma unroll
-    for (int i = 0; i < RePlan::kWOps; ++i)
-      dma16(base, w_off[i], lds_address(lds_w[0]) + buf * kWBuf + 1024 * (RePlan::kWOps * wave + i));
+    for (int i = 0; i < RePlan::kWOps; ++i) issue_w1(step4, buf, i);
   };
   // Scales of the K range: column c holds 32 dwords (groups g0 .. g0+63),
   // dword d at physical dword d ^ (c%32), so the per-step reads (32
@@ -221,37 +227,35 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
     const int d = min((g0 >> 1) + ((lane & 31) ^ (c & 31)), row_dwords - 1);
     load_lds<4>(a.s + static_cast<int64_t>(col) * a.ss0 * 2 + 4 * d, lds_address(lds_s) + 256 * i);
   };
-  // Scale of column block nt (local column 64*ni + 32*nt + li) for global
-  // group g of the range.
-  const int s_lane = kSCol * (64 * ni + li);
-  auto scale = [&](int nt, int g) -> float {
+  // Scale of this wave's column (local 32*ni + li) for global group g of the range.
+  const int s_lane = kSCol * (32 * ni + li);
+  auto scale = [&](int g) -> float {
     const int gl = g - g0;
-    const uint32_t bits = *reinterpret_cast<const uint16_t*>(lds_s + s_lane + kSCol * 32 * nt + 4 * ((gl >> 1) ^ li) +
-                                                              2 * (gl & 1));
+    const uint32_t bits =
+        *reinterpret_cast<const uint16_t*>(lds_s + s_lane + 4 * ((gl >> 1) ^ li) + 2 * (gl & 1));
     return bf16_bits_to_f32(bits);
   };
-  // A fragment (mt, kk): local row 64*mi + 32*mt + li, chunk 4*lh + kk. The
+  // A fragment (mt, kk): local row 128*mi + 32*mt + li, chunk 4*lh + kk. The
   // swizzle depends on the row only through li, so mt adds 4096 bytes.
   int a_rd[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    const int row = 64 * mi + li;
+    const int row = 128 * mi + li;
     a_rd[kk] = (row >> 3) * 1024 + (8 * (row & 7) + a_slot(row, 4 * lh + kk)) * 16;
   }
   auto read_a = [&](int stage, int mt, int kk) -> bf16x8_t {
     return *reinterpret_cast<const bf16x8_t*>(&lds_a[0][0] + stage * kAStage + a_rd[kk] + 4096 * mt);
   };
-  // The lane's four packed words of column block nt for a step with t % 4 =
-  // sub in buffer buf: local column 64*ni + 32*nt + li (nt adds 32 columns,
-  // the same swizzle), part 2*sub + lh.
+  // The lane's four packed words (local column 32*ni + li, part 2*sub + lh)
+  // of a step with t % 4 = sub, in buffer buf.
   int w_rd[4];
 #pragma unroll
   for (int sub = 0; sub < 4; ++sub) {
-    const int c = 64 * ni + li;
+    const int c = 32 * ni + li;
     w_rd[sub] = kWRun * c + 16 * w_slot(c, 2 * sub + lh);
   }
-  auto read_w = [&](int buf, int sub, int nt) -> u32x4_t {
-    return *reinterpret_cast<const u32x4_t*>(&lds_w[0][0] + buf * kWBuf + w_rd[sub] + kWRun * 32 * nt);
+  auto read_w = [&](int buf, int sub) -> u32x4_t {
+    return *reinterpret_cast<const u32x4_t*>(&lds_w[0][0] + buf * kWBuf + w_rd[sub]);
   };
 
   // Prologue, as the issue order the waits count (RePlan): scales; packed
@@ -264,11 +268,11 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   issue_a(min(1, last), 1);
   wait_vmcnt<2 * RePlan::kAOps>();  // the scales and the packed words of steps 0..3
   __syncthreads();
-  bf16x8_t bq0[4], bq1[4];  // B operands of column blocks 0 and 1, by chunk
+  bf16x8_t bq[4];  // B operands of the step, by chunk
   {
-    const u32x4_t w = read_w(0, 0, 0);
+    const u32x4_t w = read_w(0, 0);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) bq0[kk] = codes_convert(codes_split(w[kk]));
+    for (int kk = 0; kk < 4; ++kk) bq[kk] = codes_convert(codes_split(w[kk]));
   }
 
   f32x16_t y[4], acc[4];
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
       acc[T][v] = 0.0f;  // tiles 2, 3 of "step -1" are scaled by 0 in the first step
     }
   const f32x16_t zero = {};
-  float sc_prev1 = 0.0f;  // scale of column block 1 for the previous step
+  float sc_prev = 0.0f;  // scale of the previous step
 
   int stage = 0;  // t % 3
   for (int t = 0; t < steps; t += 4) {
@@ -291,61 +295,67 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
       __syncthreads();
       // Iteration tt issues the activations of step tt+2 (into the stage
       // step tt-1 used), then at tt % 4 == 0 the packed words of steps tt+4 ..
-      // tt+7 (into the buffer steps tt-4 .. tt-1 used). Past the range end
-      // the last step is fetched again into the same free places, so every
-      // iteration issues the same transfers.
-      issue_a(min(tt + 2, last), stage == 0 ? 2 : stage - 1);
-      if constexpr (J == 0) issue_w(min(tt + 4, last & ~3), ((tt >> 2) + 1) & 1);
-
-      // LDS reads two slots before their first use, so that they do not all
-      // queue behind each other at the start of the step: the fragments of
-      // chunk 0 and the packed words of column block 1 first; then in slot s
-      // < 6 the fragment slot s+2 takes; in slot 6 the packed words of column
-      // block 0 for the next step (the last step reads its own again) and the
-      // step's scales.
-      bf16x8_t af[2][4];
-      af[0][0] = read_a(stage, 0, 0);
-      af[1][0] = read_a(stage, 1, 0);
+      // tt+7 (into the buffer steps tt-4 .. tt-1 used), one instruction every
+      // other slot (slots 0, 2, 4, 6, then 8, 10) so that the workgroup's
+      // transfers do not queue up at the start of the step. Past the range
+      // end the last step is fetched again into the same free places, so
+      // every iteration issues the same transfers.
+      const int a_step = min(tt + 2, last), a_stage = stage == 0 ? 2 : stage - 1;
+      const int w_step = min(tt + 4, last & ~3), w_buf = ((tt >> 2) + 1) & 1;
+      static_assert(RePlan::kAOps == 4 && RePlan::kWOps == 2, "transfer slots below");
+      // The next step's packed words (the last step reads its own again),
+      // decoded during this step; the fragments of slots 0..2.
       const int buf = (tt >> 2) & 1;
-      const u32x4_t wv1 = read_w(buf, J, 1);
-      u32x4_t wv0;
-      float sc0, sc1;
+      const u32x4_t wvn = J == 3 ? read_w(tt + 1 <= last ? buf ^ 1 : buf, tt + 1 <= last ? 0 : 3) : read_w(buf, J + 1);
+      bf16x8_t af[16];  // by slot
+      af[0] = read_a(stage, 0, 0);
+      af[1] = read_a(stage, 1, 0);
+      af[2] = read_a(stage, 0, 1);
       constexpr bool kFirst = GSTEPS == 1 || (J & 1) == 0;     // first step of its group
       constexpr bool kLast = GSTEPS == 1 || (J & 1) == 1;      // last step of its group
       constexpr bool kPrevLast = GSTEPS == 1 || (J & 1) == 0;  // the previous step ended a group
+      bf16x8_t bqn[4];
+      uint32_t m_even = 0, m_odd = 0;
       CodePair cp;
-      Unroll<0, 16>::run([&](auto sc) {
-        constexpr int s = decltype(sc)::value;
-        constexpr int half = s / 8, rr = s % 8, kk = rr / 2, mt = rr % 2, nt = half, T = mt + 2 * nt;
-        if constexpr (s < 6) {
-          af[s % 2][s / 2 + 1] = read_a(stage, s % 2, s / 2 + 1);
-        } else if constexpr (s == 6) {
-          wv0 = J == 3 ? read_w(tt + 1 <= last ? buf ^ 1 : buf, tt + 1 <= last ? 0 : 3, 0) : read_w(buf, J + 1, 0);
-          const int g = (s0 + tt) / GSTEPS;
-          sc0 = scale(0, g);
-          sc1 = scale(1, g);
+      float sc = 0.0f;
+      Unroll<0, 16>::run([&](auto sc_) {
+        constexpr int s = decltype(sc_)::value;
+        constexpr int half = s / 8, rr = s % 8, kk = rr / 2, mt = 2 * half + rr % 2;
+        if constexpr (s % 2 == 0 && s < 8) issue_a1(a_step, a_stage, s / 2);
+        if constexpr (J == 0 && (s == 8 || s == 10)) issue_w1(w_step, w_buf, (s - 8) / 2);
+        if constexpr (s + 3 < 16) {
+          constexpr int s3 = s + 3, r3 = s3 % 8;
+          af[s3] = read_a(stage, 2 * (s3 / 8) + r3 % 2, r3 / 2);
         }
-        acc[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt][kk], nt == 0 ? bq0[kk] : bq1[kk],
-                                                         (kFirst && kk == 0) ? zero : acc[T], 0, 0, 0);
+        if constexpr (s == 4) sc = scale((s0 + tt) / GSTEPS);
+        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bq[kk], (kFirst && kk == 0) ? zero : acc[mt], 0, 0,
+                                                          0);
         // Scaling: four elements of tile 2 + rr/4 (previous step) or rr/4.
         constexpr int ST = half == 0 ? 2 + rr / 4 : rr / 4, v0 = 4 * (rr % 4);
         if constexpr (half == 0 ? kPrevLast : kLast) {
-          const float s_t = half == 0 ? sc_prev1 : sc0;
+          const float s_t = half == 0 ? sc_prev : sc;
 #pragma unroll
           for (int v = v0; v < v0 + 4; ++v) y[ST][v] = fmaf(s_t, acc[ST][v], y[ST][v]);
         }
-        // Decode: word rr/2 of column block 1 (this step) or 0 (next step).
-        const uint32_t word = (half == 0 ? wv1 : wv0)[rr / 2];
-        if constexpr (rr % 2 == 0) {
-          cp = codes_split(word);
-        } else if constexpr (half == 0) {
-          bq1[rr / 2] = codes_convert(cp);
-        } else {
-          bq0[rr / 2] = codes_convert(cp);
+        // Decode of the next step's word w in slots 2+3w (nibble masks),
+        // 3+3w (ordering), 4+3w (conversion).
+        if constexpr (s >= 2 && s < 14) {
+          constexpr int w = (s - 2) / 3, ph = (s - 2) % 3;
+          if constexpr (ph == 0) {
+            m_even = wvn[w] & 0x0f0f0f0fu;
+            m_odd = (wvn[w] >> 4) & 0x0f0f0f0fu;
+          } else if constexpr (ph == 1) {
+            cp = CodePair{__builtin_amdgcn_perm(m_odd, m_even, 0x05010400u),
+                          __builtin_amdgcn_perm(m_odd, m_even, 0x07030602u)};
+          } else {
+            bqn[w] = codes_convert(cp);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       });
-      sc_prev1 = sc1;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) bq[kk] = bqn[kk];
+      sc_prev = sc;
       stage = stage == 2 ? 0 : stage + 1;
     });
   }
@@ -386,7 +396,7 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
 #pragma unroll
   for (int T = 2; T < 4; ++T)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc_prev1, acc[T][v], y[T][v]);
+    for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc_prev, acc[T][v], y[T][v]);
   wait_vmcnt<0>();
   __syncthreads();
   // Chunk c: lane half h takes local groups 16c + 8h .. +7; entries of groups
@@ -395,20 +405,17 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
 #pragma unroll
   for (int c = 0; c < kMaxGroups / 16; ++c) {
     const int gl = 16 * c + 8 * lh;
-    u32x4_t bb[2], xv[3][2];
+    u32x4_t bb, xv[3][4];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t v = *reinterpret_cast<const uint32_t*>(lds_s + s_lane + kSCol * 32 * nt +
-                                                             4 * (((gl >> 1) + e) ^ li));
-        bb[nt][e] = gl + 2 * e < gcount ? v : 0u;
-      }
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(lds_s + s_lane + 4 * (((gl >> 1) + e) ^ li));
+      bb[e] = gl + 2 * e < gcount ? v : 0u;
+    }
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int row = 64 * mi + 32 * mt + li;
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = 128 * mi + 32 * mt + li;
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds_a[0][0] + pl * (kRows * 128) + row * 128 +
                                                             16 * a_slot(row, 2 * c + lh));
 #pragma unroll
@@ -417,38 +424,31 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          y[mt + 2 * nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][mt]),
-                                                                   __builtin_bit_cast(bf16x8_t, bb[nt]),
-                                                                   y[mt + 2 * nt], 0, 0, 0);
+      for (int mt = 0; mt < 4; ++mt)
+        y[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][mt]),
+                                                        __builtin_bit_cast(bf16x8_t, bb), y[mt], 0, 0, 0);
   }
 
-  // Accumulator (mt, nt) element v of lane l is row 8*(v/4) + 4*(l/32) + v%4
+  // Accumulator tile mt, element v of lane l is row 8*(v/4) + 4*(l/32) + v%4
   // and column l%32 of its 32x32 tile. Offsets are 32-bit from the tile's
   // first row (256 rows * N * 4 < 2^31).
   const bool full = m0 + kRows <= a.M;
   float* base = (a.splits == 1 ? a.out : a.partial + split * static_cast<int64_t>(a.M) * a.N) +
                 static_cast<int64_t>(m0) * a.N;
+  const int col = n0 + 32 * ni + li;
   with_store_kind(a.splits == 1 ? a.epi.kind : kEpiNone, [&](auto kind) {
     constexpr int KIND = decltype(kind)::value;
+    if (col < a.N) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = n0 + 64 * ni + 32 * nt + li;
-      if (col < a.N) {
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int rr = 64 * mi + 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
-            if (full || m0 + rr < a.M) {
-              const uint32_t off = static_cast<uint32_t>(rr * a.N + col) * 4u;
-              store_as<KIND>(a.epi, reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(base) + off), col,
-                             y[mt + 2 * nt][v]);
-            }
+        for (int v = 0; v < 16; ++v) {
+          const int rr = 128 * mi + 32 * mt + 8 * (v / 4) + 4 * lh + (v % 4);
+          if (full || m0 + rr < a.M) {
+            const uint32_t off = static_cast<uint32_t>(rr * a.N + col) * 4u;
+            store_as<KIND>(a.epi, reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(base) + off), col, y[mt][v]);
           }
-      }
+        }
     }
   });
 }
