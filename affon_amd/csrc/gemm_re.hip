@@ -52,6 +52,7 @@ constexpr int kWRun = 128;                 // packed bytes per column and four s
 constexpr int kWBuf = kCols * kWRun;
 constexpr int kSCol = 128;                 // scale bytes per column for the K range (32 dwords)
 constexpr int kMaxGroups = kSCol / 2;      // bf16 scales per column and K range
+constexpr int kMinRangeSteps = 16;         // shortest K range worth the kernel's fixed costs
 
 static_assert(kRows / 8 / kReWaves == RePlan::kAOps, "8-row activation transfers per wave and step");
 static_assert(kWBuf / 1024 / kReWaves == RePlan::kWOps, "packed-word transfers per wave and four steps");
@@ -486,7 +487,11 @@ bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status) {
   const int gsteps = static_cast<int>(p.group / kBK);
   const int tiles = ((N + kCols - 1) / kCols) * ((M + kRows - 1) / kRows);
   const int splits = re_splits(tiles, steps, gsteps);
-  if (splits == 0) return false;
+  // A K range of fewer than 16 steps leaves too little loop for the kernel's
+  // fixed costs (group-sum pre-pass, prologue, bias term, partial sums): the
+  // row-tiled decode kernel is faster there (e.g. 128 x 4096 x 4096: 15.7
+  // against 31.4 us).
+  if (splits == 0 || steps / splits < kMinRangeSteps) return false;
   const int range_groups = steps / splits / gsteps;
   const size_t partial_bytes = splits > 1 ? static_cast<size_t>(splits) * M * N * 4 : 0;
   const size_t plane_bytes = static_cast<size_t>(splits) * 3 * M * kMaxGroups * 2;

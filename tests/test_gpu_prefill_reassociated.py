@@ -40,13 +40,16 @@ def product_f64(x, q, s, b, group, cols):
     return x @ w.T
 
 
-# (M, N, K, group): partial tiles with two and four K ranges; the full-size
-# down projection (four ranges of 56 groups); the full-size gate/up
-# projection (one range of 64 groups); eight ranges of 32 and of 16 groups;
-# two ranges where the tile count alone would take one range of 128 groups.
+# (M, N, K, group): a half row tile and a partial column tile over eight K
+# ranges of 16 steps; partial tiles over eight ranges of 16 groups; seven
+# ranges of 8 groups (half a bias-term chunk); the full-size down projection
+# (four ranges of 56 groups); the full-size gate/up projection (one range of
+# 64 groups); eight ranges of 32 and of 16 groups; two ranges where the tile
+# count alone would take one range of 128 groups.
 EXACT_SHAPES = [
-    (128, 200, 1024, 64),
-    (300, 130, 2048, 128),
+    (128, 200, 8192, 64),
+    (300, 130, 16384, 128),
+    (200, 300, 7168, 128),
     (512, 4096, 14336, 64),
     (512, 14336, 4096, 64),
     (256, 384, 16384, 64),
@@ -104,3 +107,35 @@ def test_reassociated_prefill_deterministic(session):
         first = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=64).numpy()
         for _ in range(2):
             np.testing.assert_array_equal(A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=64).numpy(), first)
+
+
+def test_reassociated_prefill_epilogues_one_range(session, rng):
+    """Output bias (f32 and bf16) and the SiLU-gated product stored by the
+    kernel itself (one K range: 192 tiles of 256 x 128): the fused outputs
+    against the plain outputs with the epilogue applied here (the bias add is
+    the same f32 add, so bit-exact; silu(g) * u within 6 ulp of its f64
+    value), and the plain output against f64 on a column subset."""
+    M, N, K, group = 256, 24576, 1024, 128
+    x, gp, gs, gb = seeded_problem(M, N, K, 4, group, "bf16", "bf16", seed=23)
+    _, upk, us, ub = seeded_problem(M, N, K, 4, group, "bf16", "bf16", seed=29)
+    xt = upload(session, x, "bf16")
+    gate = tuple(upload(session, a, dtype_of(a)) for a in (gp, gs, gb))
+    up = tuple(upload(session, a, dtype_of(a)) for a in (upk, us, ub))
+    assert A.selected_implementation(xt, *gate, bits=4, group_size=group) == GEMV_MFMA
+    g = A.quantized_matmul(xt, *gate, bits=4, group_size=group).numpy()
+    u = A.quantized_matmul(xt, *up, bits=4, group_size=group).numpy()
+    cols = np.unique(np.linspace(0, N - 1, 256).astype(int))
+    assert accuracy_ratio(g, x, gp, gs, gb, group, cols) <= 2.0 ** -18
+    for bias_dtype in ("f32", "bf16"):
+        bias_values = rng.standard_normal(N).astype(np.float32)
+        bias = storage(bias_values, "bf16") if bias_dtype == "bf16" else bias_values
+        fused = A.quantized_linear(xt, *gate, upload(session, bias, bias_dtype), bits=4, group_size=group).numpy()
+        np.testing.assert_array_equal(fused, (g + widened(bias).astype(np.float32)).astype(np.float32),
+                                      err_msg=bias_dtype)
+    fused = A.quantized_silu_gate(xt, gate, up, bits=4, group_size=group).numpy()
+    g64 = g.astype(np.float64)
+    with np.errstate(over="ignore"):
+        expected = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
+    bound = 6 * np.spacing(np.abs(expected).astype(np.float32)).astype(np.float64) + 1e-30
+    err = np.abs(fused.astype(np.float64) - expected)
+    assert np.all(err <= bound), f"worst {float(err.max())}"

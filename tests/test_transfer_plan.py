@@ -1,7 +1,7 @@
-"""The counted waits of the tiled kernels' transfer plan (lds_pipeline.h
+"""The counted waits of the tiled kernels' transfer plans (lds_pipeline.h
 Plan::wait_own for the decode-batch kernel, Plan::wait and the prologue
-wait for the prefill GEMM) against an independent simulation of the issue
-stream.
+wait for the prefill GEMM, RePlan::wait for the reassociated prefill GEMM)
+against an independent simulation of the issue stream.
 
 The simulation lists every transfer instruction the kernels issue, in
 order, with the K steps whose data it carries (parameter windows, packed
@@ -51,6 +51,9 @@ void dump(const char* name) {
 }
 int main() {
 @CALLS@
+  std::printf("replan");
+  for (int j = 0; j < 4; ++j) std::printf(" %d", RePlan::wait(j));
+  std::printf(" %d %d %d\n", RePlan::kAOps, RePlan::kWOps, RePlan::kSOps);
   return 0;
 }
 """
@@ -79,7 +82,10 @@ def plan_values(tmp_path_factory):
     for line in out.splitlines():
         name, *nums = line.split()
         nums = list(map(int, nums))
-        values[name] = {"own": nums[0:4], "wait": nums[4:8], "prologue": nums[8]}
+        if name == "replan":
+            values[name] = {"wait": nums[0:4], "aops": nums[4], "wops": nums[5], "sops": nums[6]}
+        else:
+            values[name] = {"own": nums[0:4], "wait": nums[4:8], "prologue": nums[8]}
     return values
 
 
@@ -153,3 +159,33 @@ def test_simulation_detects_a_wait_one_too_large(plan_values):
     own = plan_values[name]["own"]
     sim = allowed_in_flight(ops, 12, {("a", 12), ("w", 12), ("p", 12)})
     assert own[0] == sim and not (own[0] + 1 <= sim)
+
+
+def re_issue_stream(aops, wops, sops, iterations):
+    """The reassociated prefill GEMM (gemm_re.hip), one wave, in issue order:
+    the K range's scales; the packed words of steps 0..3; the activations of
+    steps 0 and 1; then iteration t issues the activations of step t+2 and, at
+    t % 4 == 0, the packed words of steps t+4 .. t+7."""
+    ops = [(-3, "p", None)] * sops + [(-3, "w", {0, 1, 2, 3})] * wops
+    ops += [(-2, "a", {0})] * aops + [(-1, "a", {1})] * aops
+    for t in range(iterations):
+        ops += [(t, "a", {t + 2})] * aops
+        if t % 4 == 0:
+            ops += [(t, "w", set(range(t + 4, t + 8)))] * wops
+    return ops
+
+
+def test_reassociated_gemm_waits(plan_values):
+    v = plan_values["replan"]
+    ops = re_issue_stream(v["aops"], v["wops"], v["sops"], 40)
+    # Before the loop the kernel decodes step 0's packed words after waiting
+    # for all but the two activation transfers (2 * aops).
+    assert 2 * v["aops"] == allowed_in_flight(ops, 0, {("w", 0), ("p", 0)})
+    # Iteration t reads step t's activations, packed words and scales, and the
+    # next step's packed words (decoded one step ahead).
+    for t in range(0, 32):
+        needs = {("a", t), ("w", t), ("w", t + 1), ("p", t)}
+        sim = allowed_in_flight(ops, t, needs)
+        assert v["wait"][t % 4] <= sim, (t, v["wait"][t % 4], sim)
+        if t >= 4:
+            assert v["wait"][t % 4] == sim, (t, v["wait"][t % 4], sim)
