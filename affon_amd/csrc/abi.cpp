@@ -253,8 +253,9 @@ bool policy_accepts(int policy, int numerical_class) {
 
 // Shape rule for AUTO among candidates that pass their guards: the prefill
 // GEMM for M >= 64 (when the policy admits its approximate class), the MFMA
-// decode kernels for M >= 2 with bf16 input (row tiles of 32 beyond 32 rows:
-// the reassociated class's path for prefill), the VALU decode kernel
+// decode kernels for M >= 2 with bf16 input (the reassociated class's path
+// for prefill: from 128 rows the large-tile reassociated GEMM, gemm_re.hip,
+// where it takes the shape, else row tiles of 32), the VALU decode kernel
 // otherwise, the generic kernel last.
 bool auto_prefers(const Candidate& c, const affon::QmmProblem& p) {
   switch (c.impl) {
