@@ -334,6 +334,13 @@ bool mfma_supports(const QmmProblem& p) {
 }
 
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
+  // 4-bit weights with bf16 parameters, groups of 64 or 128: the 8-wave GEMM
+  // of gemm_re.hip in its rounded-weight form, where its K ranges are long
+  // enough; then the pair kernel for the other 4-bit shapes above 128 rows.
+  if (p.M >= 128 && re_gemm_supports(p)) {
+    hipError_t e = hipSuccess;
+    if (re_gemm_launch(p, l, &e, true)) return e;
+  }
   if (p.M > 128 && pair_supports(p)) return pair_launch(p, l);
   hipStream_t stream = l.stream;
   TileArgs a;

@@ -134,7 +134,21 @@ __device__ __forceinline__ bf16x8_t codes_convert(CodePair p) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// GSTEPS: K steps per group (1: group 64, 2: group 128).
+// B operand of the ROUNDED mode from one packed word: bf16(s * q + b) for its
+// eight codes in k order (s carries the 2^9 of the FP8 reading of a code).
+__device__ __forceinline__ bf16x8_t weights_rounded(uint32_t w, float s, float b) {
+  const uint32_t even = w & 0x0f0f0f0fu, odd = (w >> 4) & 0x0f0f0f0fu;
+  const f32x2_t e0 = __builtin_amdgcn_cvt_pk_f32_fp8(even, false), e1 = __builtin_amdgcn_cvt_pk_f32_fp8(even, true);
+  const f32x2_t o0 = __builtin_amdgcn_cvt_pk_f32_fp8(odd, false), o1 = __builtin_amdgcn_cvt_pk_f32_fp8(odd, true);
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{pack_bf16(fmaf(e0.x, s, b), fmaf(o0.x, s, b)),
+                                              pack_bf16(fmaf(e0.y, s, b), fmaf(o0.y, s, b)),
+                                              pack_bf16(fmaf(e1.x, s, b), fmaf(o1.x, s, b)),
+                                              pack_bf16(fmaf(e1.y, s, b), fmaf(o1.y, s, b))});
+}
+
+// GSTEPS: K steps per group (1: group 64, 2: group 128). ROUNDED: the
+// approximate class instead -- decoded weights bf16(s*q + b) in the B
+// operand, accumulated straight into y; no group sums, no bias term.
 //
 // Waves: 2 (rows) x 4 (columns); wave (mi, ni) computes rows 128*mi .. +127
 // and columns 32*ni .. +31 of the tile as accumulator tiles T = 0..3 (rows
@@ -150,12 +164,13 @@ __device__ __forceinline__ bf16x8_t codes_convert(CodePair p) {
 // group-sum accumulators suffices and the matrix core and the vector ALU
 // work side by side within a wave. Each A fragment feeds one MFMA and is read
 // from LDS three slots ahead of it.
-template <int GSTEPS>
+template <int GSTEPS, bool ROUNDED>
 __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   const TileArgs& a = r.t;
   __shared__ __attribute__((aligned(16))) uint8_t lds_a[kAStages][kAStage];
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[2][kWBuf];
   __shared__ __attribute__((aligned(16))) uint8_t lds_s[kCols * kSCol];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b[ROUNDED ? kCols * kSCol : 16];  // ROUNDED: biases
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -220,22 +235,24 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   // consecutive columns, one group) hit distinct banks. Instruction i, lane L
   // writes dword 64i + L: column 2i + L/32, physical dword L%32. Dwords past
   // the row end repeat the row's last dword.
-  auto issue_s = [&](int ii) {
+  // (ROUNDED: the biases the same way into lds_b.)
+  auto issue_p = [&](const uint8_t* src, int64_t row_stride, uint8_t* dst, int ii) {
     const int i = RePlan::kSOps * wave + ii;
     const int c = 2 * i + (lane >> 5);
     const int col = min(n0 + c, a.N - 1);
     const int row_dwords = (a.K >> (5 + a.group_shift)) / 2;
     const int d = min((g0 >> 1) + ((lane & 31) ^ (c & 31)), row_dwords - 1);
-    load_lds<4>(a.s + static_cast<int64_t>(col) * a.ss0 * 2 + 4 * d, lds_address(lds_s) + 256 * i);
+    load_lds<4>(src + static_cast<int64_t>(col) * row_stride * 2 + 4 * d, lds_address(dst) + 256 * i);
   };
+  auto issue_s = [&](int ii) { issue_p(a.s, a.ss0, lds_s, ii); };
   // Scale of this wave's column (local 32*ni + li) for global group g of the range.
   const int s_lane = kSCol * (32 * ni + li);
-  auto scale = [&](int g) -> float {
+  auto param = [&](const uint8_t* lds, int g) -> float {
     const int gl = g - g0;
-    const uint32_t bits =
-        *reinterpret_cast<const uint16_t*>(lds_s + s_lane + 4 * ((gl >> 1) ^ li) + 2 * (gl & 1));
+    const uint32_t bits = *reinterpret_cast<const uint16_t*>(lds + s_lane + 4 * ((gl >> 1) ^ li) + 2 * (gl & 1));
     return bf16_bits_to_f32(bits);
   };
+  auto scale = [&](int g) -> float { return param(lds_s, g); };
   // A fragment (mt, kk): local row 128*mi + 32*mt + li, chunk 4*lh + kk. The
   // swizzle depends on the row only through li, so mt adds 4096 bytes.
   int a_rd[4];
@@ -264,6 +281,10 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   // column block 0 for step 0 (the loop decodes them one step ahead).
 #pragma unroll
   for (int ii = 0; ii < RePlan::kSOps; ++ii) issue_s(ii);
+  if constexpr (ROUNDED) {
+#pragma unroll
+    for (int ii = 0; ii < RePlan::kSOps; ++ii) issue_p(a.b, a.bs0, lds_b, ii);
+  }
   issue_w(0, 0);
   issue_a(0, 0);
   issue_a(min(1, last), 1);
@@ -272,8 +293,14 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
   bf16x8_t bq[4];  // B operands of the step, by chunk
   {
     const u32x4_t w = read_w(0, 0);
+    if constexpr (ROUNDED) {
+      const float s_0 = scale(s0 / GSTEPS) * 512.0f, b_0 = param(lds_b, s0 / GSTEPS);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) bq[kk] = codes_convert(codes_split(w[kk]));
+      for (int kk = 0; kk < 4; ++kk) bq[kk] = weights_rounded(w[kk], s_0, b_0);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) bq[kk] = codes_convert(codes_split(w[kk]));
+    }
   }
 
   f32x16_t y[4], acc[4];
@@ -318,7 +345,9 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
       bf16x8_t bqn[4];
       uint32_t m_even = 0, m_odd = 0;
       CodePair cp;
+      f32x2_t ce[2], co[2];  // ROUNDED: converted codes (even, odd) of one word
       float sc = 0.0f;
+      float sn = 0.0f, bn = 0.0f;  // ROUNDED: scale (times 2^9) and bias of the next step's group
       Unroll<0, 16>::run([&](auto sc_) {
         constexpr int s = decltype(sc_)::value;
         constexpr int half = s / 8, rr = s % 8, kk = rr / 2, mt = 2 * half + rr % 2;
@@ -328,19 +357,48 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
           constexpr int s3 = s + 3, r3 = s3 % 8;
           af[s3] = read_a(stage, 2 * (s3 / 8) + r3 % 2, r3 / 2);
         }
-        if constexpr (s == 4) sc = scale((s0 + tt) / GSTEPS);
-        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bq[kk], (kFirst && kk == 0) ? zero : acc[mt], 0, 0,
-                                                          0);
+        if constexpr (!ROUNDED && s == 4) sc = scale((s0 + tt) / GSTEPS);
+        if constexpr (ROUNDED && s == 0) {
+          const int gn = (s0 + min(tt + 1, last)) / GSTEPS;
+          sn = scale(gn) * 512.0f;
+          bn = param(lds_b, gn);
+        }
+        if constexpr (ROUNDED)
+          y[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bq[kk], y[mt], 0, 0, 0);
+        else
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bq[kk], (kFirst && kk == 0) ? zero : acc[mt], 0,
+                                                            0, 0);
         // Scaling: four elements of tile 2 + rr/4 (previous step) or rr/4.
         constexpr int ST = half == 0 ? 2 + rr / 4 : rr / 4, v0 = 4 * (rr % 4);
-        if constexpr (half == 0 ? kPrevLast : kLast) {
+        if constexpr (!ROUNDED && (half == 0 ? kPrevLast : kLast)) {
           const float s_t = half == 0 ? sc_prev : sc;
 #pragma unroll
           for (int v = v0; v < v0 + 4; ++v) y[ST][v] = fmaf(s_t, acc[ST][v], y[ST][v]);
         }
         // Decode of the next step's word w in slots 2+3w (nibble masks),
         // 3+3w (ordering), 4+3w (conversion).
-        if constexpr (s >= 2 && s < 14) {
+        if constexpr (ROUNDED && s >= 2 && s < 14) {
+          // ROUNDED: nibble masks and the even codes' conversion; the odd
+          // codes' conversion and dwords 0, 1; dwords 2, 3 of bf16(s*q + b).
+          constexpr int w = (s - 2) / 3, ph = (s - 2) % 3;
+          if constexpr (ph == 0) {
+            m_even = wvn[w] & 0x0f0f0f0fu;
+            m_odd = (wvn[w] >> 4) & 0x0f0f0f0fu;
+            ce[0] = __builtin_amdgcn_cvt_pk_f32_fp8(m_even, false);  // codes 0, 2
+            ce[1] = __builtin_amdgcn_cvt_pk_f32_fp8(m_even, true);   // codes 4, 6
+          } else if constexpr (ph == 1) {
+            co[0] = __builtin_amdgcn_cvt_pk_f32_fp8(m_odd, false);  // codes 1, 3
+            co[1] = __builtin_amdgcn_cvt_pk_f32_fp8(m_odd, true);   // codes 5, 7
+            bqn[w] = __builtin_bit_cast(bf16x8_t, u32x4_t{pack_bf16(fmaf(ce[0].x, sn, bn), fmaf(co[0].x, sn, bn)),
+                                                          pack_bf16(fmaf(ce[0].y, sn, bn), fmaf(co[0].y, sn, bn)), 0u,
+                                                          0u});
+          } else {
+            u32x4_t v = __builtin_bit_cast(u32x4_t, bqn[w]);
+            v[2] = pack_bf16(fmaf(ce[1].x, sn, bn), fmaf(co[1].x, sn, bn));
+            v[3] = pack_bf16(fmaf(ce[1].y, sn, bn), fmaf(co[1].y, sn, bn));
+            bqn[w] = __builtin_bit_cast(bf16x8_t, v);
+          }
+        } else if constexpr (!ROUNDED && s >= 2 && s < 14) {
           constexpr int w = (s - 2) / 3, ph = (s - 2) % 3;
           if constexpr (ph == 0) {
             m_even = wvn[w] & 0x0f0f0f0fu;
@@ -360,74 +418,78 @@ __global__ __launch_bounds__(kReThreads) void qgemm_re_kernel(ReArgs r) {
       stage = stage == 2 ? 0 : stage + 1;
     });
   }
-  // Bias term: y += sum over the range's groups of X_t[row][g] * b[col][g],
-  // 16 groups per MFMA. Its operands go through LDS, brought by whole-line
-  // transfers once every wave is done with the loop's buffers: the tile's
-  // rows of the three planes (this range's 128-byte rows, groups g0 ..
-  // g0+63) into the activation ring, plane t at 32 KiB * t, row r at 128 * r,
-  // 16-byte slot q at a_slot(r, q); the tile's biases into the scale area
-  // with the scales' layout.
-  wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
-  __syncthreads();
-  {
-    static_assert(3 * kRows * 128 <= kAStages * kAStage, "three plane tiles fit the activation ring");
-    static_assert(3 * kRows / 8 % kReWaves == 0, "whole plane transfers per wave");
-    constexpr int kXOps = 3 * kRows / 8 / kReWaves;
-    const uint16_t* planes = r.planes + static_cast<int64_t>(split) * 3 * a.M * kMaxGroups;
-#pragma unroll
-    for (int ii = 0; ii < kXOps; ++ii) {
-      const int i = kXOps * wave + ii;  // plane i / 32, rows 8*(i%32) ..
-      const int pl = i / (kRows / 8), rg = i % (kRows / 8);
-      const int row = min(m0 + 8 * rg + (lane >> 3), a.M - 1);
-      const int q = (lane & 7) ^ (lane >> 3) ^ (rg & 1);
-      load_lds<16>(planes + (static_cast<int64_t>(pl) * a.M + row) * kMaxGroups + 8 * q,
-                   lds_address(lds_a[0]) + pl * (kRows * 128) + 1024 * rg);
-    }
-    const int row_dwords = (a.K >> (5 + a.group_shift)) / 2;
-#pragma unroll
-    for (int ii = 0; ii < RePlan::kSOps; ++ii) {
-      const int i = RePlan::kSOps * wave + ii;
-      const int c = 2 * i + (lane >> 5);
-      const int col = min(n0 + c, a.N - 1);
-      const int d = min((g0 >> 1) + ((lane & 31) ^ (c & 31)), row_dwords - 1);
-      load_lds<4>(a.b + static_cast<int64_t>(col) * a.bs0 * 2 + 4 * d, lds_address(lds_s) + 256 * i);
-    }
-  }
-  // Tiles 2, 3 of the last step (the range ends a group), while the transfers fly.
-#pragma unroll
-  for (int T = 2; T < 4; ++T)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc_prev, acc[T][v], y[T][v]);
-  wait_vmcnt<0>();
-  __syncthreads();
-  // Chunk c: lane half h takes local groups 16c + 8h .. +7; entries of groups
-  // past the range are replaced by zeros on both sides.
-  const int gcount = g1 - g0;
-#pragma unroll
-  for (int c = 0; c < kMaxGroups / 16; ++c) {
-    const int gl = 16 * c + 8 * lh;
-    u32x4_t bb, xv[3][4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(lds_s + s_lane + 4 * (((gl >> 1) + e) ^ li));
-      bb[e] = gl + 2 * e < gcount ? v : 0u;
-    }
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int row = 128 * mi + 32 * mt + li;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds_a[0][0] + pl * (kRows * 128) + row * 128 +
-                                                            16 * a_slot(row, 2 * c + lh));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xv[pl][mt][e] = gl + 2 * e < gcount ? v[e] : 0u;
+  if constexpr (ROUNDED) {
+    wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
+  } else {
+    // Bias term: y += sum over the range's groups of X_t[row][g] * b[col][g],
+    // 16 groups per MFMA. Its operands go through LDS, brought by whole-line
+    // transfers once every wave is done with the loop's buffers: the tile's
+    // rows of the three planes (this range's 128-byte rows, groups g0 ..
+    // g0+63) into the activation ring, plane t at 32 KiB * t, row r at 128 * r,
+    // 16-byte slot q at a_slot(r, q); the tile's biases into the scale area
+    // with the scales' layout.
+    wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
+    __syncthreads();
+    {
+      static_assert(3 * kRows * 128 <= kAStages * kAStage, "three plane tiles fit the activation ring");
+      static_assert(3 * kRows / 8 % kReWaves == 0, "whole plane transfers per wave");
+      constexpr int kXOps = 3 * kRows / 8 / kReWaves;
+      const uint16_t* planes = r.planes + static_cast<int64_t>(split) * 3 * a.M * kMaxGroups;
+  #pragma unroll
+      for (int ii = 0; ii < kXOps; ++ii) {
+        const int i = kXOps * wave + ii;  // plane i / 32, rows 8*(i%32) ..
+        const int pl = i / (kRows / 8), rg = i % (kRows / 8);
+        const int row = min(m0 + 8 * rg + (lane >> 3), a.M - 1);
+        const int q = (lane & 7) ^ (lane >> 3) ^ (rg & 1);
+        load_lds<16>(planes + (static_cast<int64_t>(pl) * a.M + row) * kMaxGroups + 8 * q,
+                     lds_address(lds_a[0]) + pl * (kRows * 128) + 1024 * rg);
       }
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        y[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][mt]),
-                                                        __builtin_bit_cast(bf16x8_t, bb), y[mt], 0, 0, 0);
+      const int row_dwords = (a.K >> (5 + a.group_shift)) / 2;
+  #pragma unroll
+      for (int ii = 0; ii < RePlan::kSOps; ++ii) {
+        const int i = RePlan::kSOps * wave + ii;
+        const int c = 2 * i + (lane >> 5);
+        const int col = min(n0 + c, a.N - 1);
+        const int d = min((g0 >> 1) + ((lane & 31) ^ (c & 31)), row_dwords - 1);
+        load_lds<4>(a.b + static_cast<int64_t>(col) * a.bs0 * 2 + 4 * d, lds_address(lds_s) + 256 * i);
+      }
+    }
+    // Tiles 2, 3 of the last step (the range ends a group), while the transfers fly.
+  #pragma unroll
+    for (int T = 2; T < 4; ++T)
+  #pragma unroll
+      for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc_prev, acc[T][v], y[T][v]);
+    wait_vmcnt<0>();
+    __syncthreads();
+    // Chunk c: lane half h takes local groups 16c + 8h .. +7; entries of groups
+    // past the range are replaced by zeros on both sides.
+    const int gcount = g1 - g0;
+  #pragma unroll
+    for (int c = 0; c < kMaxGroups / 16; ++c) {
+      const int gl = 16 * c + 8 * lh;
+      u32x4_t bb, xv[3][4];
+  #pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(lds_s + s_lane + 4 * (((gl >> 1) + e) ^ li));
+        bb[e] = gl + 2 * e < gcount ? v : 0u;
+      }
+  #pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+  #pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const int row = 128 * mi + 32 * mt + li;
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds_a[0][0] + pl * (kRows * 128) + row * 128 +
+                                                              16 * a_slot(row, 2 * c + lh));
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) xv[pl][mt][e] = gl + 2 * e < gcount ? v[e] : 0u;
+        }
+  #pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+  #pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          y[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][mt]),
+                                                          __builtin_bit_cast(bf16x8_t, bb), y[mt], 0, 0, 0);
+    }
   }
 
   // Accumulator tile mt, element v of lane l is row 8*(v/4) + 4*(l/32) + v%4
@@ -480,25 +542,27 @@ bool re_gemm_supports(const QmmProblem& p) {
   return true;
 }
 
-bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status) {
-  if (!l.can_split()) return false;
+bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status, bool rounded) {
   const int M = static_cast<int>(p.M), N = static_cast<int>(p.N), K = static_cast<int>(p.K);
   const int steps = K / kBK;
   const int gsteps = static_cast<int>(p.group / kBK);
   const int tiles = ((N + kCols - 1) / kCols) * ((M + kRows - 1) / kRows);
-  const int splits = re_splits(tiles, steps, gsteps);
+  const int splits = l.can_split() ? re_splits(tiles, steps, gsteps) : (steps / gsteps <= kMaxGroups ? 1 : 0);
   // A K range of fewer than 16 steps leaves too little loop for the kernel's
-  // fixed costs (group-sum pre-pass, prologue, bias term, partial sums): the
-  // row-tiled decode kernel is faster there (e.g. 128 x 4096 x 4096: 15.7
-  // against 31.4 us).
+  // fixed costs (prologue, partial sums; for the reassociated class also the
+  // group-sum pre-pass and the bias term): the other kernels of the class
+  // are faster there (e.g. 128 x 4096 x 4096 on the row-tiled decode kernel:
+  // 15.7 against 31.4 us).
   if (splits == 0 || steps / splits < kMinRangeSteps) return false;
   const int range_groups = steps / splits / gsteps;
   const size_t partial_bytes = splits > 1 ? static_cast<size_t>(splits) * M * N * 4 : 0;
-  const size_t plane_bytes = static_cast<size_t>(splits) * 3 * M * kMaxGroups * 2;
+  const size_t plane_bytes = rounded ? 0 : static_cast<size_t>(splits) * 3 * M * kMaxGroups * 2;
   const size_t total = ((partial_bytes + 255) & ~size_t(255)) + plane_bytes;
-  if (l.fixed != nullptr && total > l.fixed_bytes) return false;  // the caller's other path runs instead
-  uint8_t* scratch = static_cast<uint8_t*>(l.scratch(total));
-  if (scratch == nullptr) return false;
+  uint8_t* scratch = nullptr;
+  if (total > 0) {
+    if (l.fixed != nullptr && total > l.fixed_bytes) return false;  // the caller's other path runs instead
+    if (!l.can_split() || (scratch = static_cast<uint8_t*>(l.scratch(total))) == nullptr) return false;
+  }
 
   ReArgs r;
   TileArgs& a = r.t;
@@ -519,17 +583,23 @@ bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status) {
   a.splits = splits;
   a.split_steps = steps / splits;
   a.partial = splits > 1 ? reinterpret_cast<float*>(scratch) : nullptr;
-  r.planes = reinterpret_cast<const uint16_t*>(scratch + ((partial_bytes + 255) & ~size_t(255)));
+  r.planes = rounded ? nullptr : reinterpret_cast<const uint16_t*>(scratch + ((partial_bytes + 255) & ~size_t(255)));
 
-  const int64_t chunks = static_cast<int64_t>(M) * (K / 8);
-  hipLaunchKernelGGL(group_sums_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, l.stream,
-                     a.x, a.xs0, M, K, static_cast<int>(p.group), range_groups, const_cast<uint16_t*>(r.planes));
-  hipError_t e = hipGetLastError();
+  hipError_t e = hipSuccess;
+  if (!rounded) {
+    const int64_t chunks = static_cast<int64_t>(M) * (K / 8);
+    hipLaunchKernelGGL(group_sums_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, l.stream,
+                       a.x, a.xs0, M, K, static_cast<int>(p.group), range_groups, const_cast<uint16_t*>(r.planes));
+    e = hipGetLastError();
+  }
   if (e == hipSuccess) {
-    if (gsteps == 1)
-      hipLaunchKernelGGL(qgemm_re_kernel<1>, dim3(tiles * splits), dim3(kReThreads), 0, l.stream, r);
+    const dim3 grid(tiles * splits), block(kReThreads);
+    if (rounded)
+      hipLaunchKernelGGL((gsteps == 1 ? qgemm_re_kernel<1, true> : qgemm_re_kernel<2, true>), grid, block, 0,
+                         l.stream, r);
     else
-      hipLaunchKernelGGL(qgemm_re_kernel<2>, dim3(tiles * splits), dim3(kReThreads), 0, l.stream, r);
+      hipLaunchKernelGGL((gsteps == 1 ? qgemm_re_kernel<1, false> : qgemm_re_kernel<2, false>), grid, block, 0,
+                         l.stream, r);
     e = hipGetLastError();
   }
   if (e == hipSuccess && splits > 1) e = launch_reduce(a, l.stream);

@@ -423,7 +423,7 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
   // (per-group activation sums) can be had.
   if (p.M >= kReMinRows && re_gemm_supports(p)) {
     hipError_t e = hipSuccess;
-    if (re_gemm_launch(p, l, &e)) return e;
+    if (re_gemm_launch(p, l, &e, false)) return e;
   }
   return tiled_launch(p, nullptr, 0, l);
 }

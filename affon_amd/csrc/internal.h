@@ -108,8 +108,11 @@ hipError_t gemv_mfma_group_launch(const QmmProblem* group, int count, const Laun
 // scale applied in f32, the bias term from per-group activation sums.
 bool re_gemm_supports(const QmmProblem& p);
 // Enqueues it and returns true (*status: the launch status), or returns
-// false with nothing enqueued when its scratch memory cannot be had now.
-bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status);
+// false with nothing enqueued when the shape's K ranges are too short for it
+// or its scratch memory cannot be had now. `rounded`: the same kernel in the
+// approximate class (decoded weights rounded to bf16, no per-group scaling),
+// which mfma_launch runs.
+bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status, bool rounded);
 
 bool mfma_supports(const QmmProblem& p);
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l);

@@ -139,3 +139,44 @@ def test_reassociated_prefill_epilogues_one_range(session, rng):
     bound = 6 * np.spacing(np.abs(expected).astype(np.float32)).astype(np.float64) + 1e-30
     err = np.abs(fused.astype(np.float64) - expected)
     assert np.all(err <= bound), f"worst {float(err.max())}"
+
+
+# ---- the same kernel in the approximate class (implementation "mfma") ----------------
+
+MFMA = "rocm_quantized_matmul.mfma"
+
+
+@pytest.mark.parametrize("shape", EXACT_SHAPES, ids=lambda s: "m{}_n{}_k{}_g{}".format(*s))
+def test_rounded_prefill_exact(session, shape, rng):
+    """Under the approximate policy the kernel rounds each decoded weight
+    s*q + b to bf16. Power-of-two scales, integer biases in [-2, 2] and codes
+    below 16 keep every decoded weight exact in bf16 (multiples of 1/8 below
+    18), so with integer activations the output must equal the f64 product."""
+    M, N, K, group = shape
+    x, q, s, b = exact_operands(rng, M, N, K, group)
+    xt = upload(session, storage(x, "bf16"), "bf16")
+    wt = upload(session, pack_codes(q, 4), "u32")
+    st, bt = upload(session, storage(s, "bf16"), "bf16"), upload(session, storage(b, "bf16"), "bf16")
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=group, policy="approximate") == MFMA
+    out = session.empty("f32", (M, N))
+    A.quantized_matmul_into(out, xt, wt, st, bt, bits=4, group_size=group, implementation="mfma",
+                            policy="approximate")
+    cols = np.unique(np.concatenate([np.arange(min(N, 160)), np.linspace(0, N - 1, 96).astype(int)]))
+    np.testing.assert_array_equal(out.numpy()[:, cols], product_f64(x, q, s, b, group, cols).astype(np.float32),
+                                  err_msg=f"{shape}")
+
+
+@pytest.mark.parametrize("M,N,K,group", [(512, 1024, 4096, 64), (300, 640, 8192, 128)])
+def test_rounded_prefill_against_oracle_and_default(session, M, N, K, group):
+    """Seeded inputs: the approximate policy's output within the bf16-product
+    tolerance of the oracle (rtol 1e-2, atol 1e-2 * rms) and of the default
+    policy's output on every element."""
+    from tests.helpers import assert_bf16_product_close, oracle_columns
+    x, packed, s, b = seeded_problem(M, N, K, 4, group, "bf16", "bf16", seed=31)
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    approx = session.empty("f32", (M, N))
+    A.quantized_matmul_into(approx, xt, wt, st, bt, bits=4, group_size=group, policy="approximate")
+    default = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=group).numpy()
+    cols = np.unique(np.linspace(0, N - 1, 256).astype(int))
+    assert_bf16_product_close(approx.numpy()[:, cols], oracle_columns(x, packed, s, b, 4, group, cols))
+    assert_bf16_product_close(approx.numpy(), default)
