@@ -1,14 +1,16 @@
-// rocm_quantized_matmul.gemv_mfma for prefill: the reassociated class on a
-// large-tile GEMM (4-bit codes, bf16 activations and parameters, groups of 64
-// or 128).
+// Prefill GEMM for 4-bit codes, bf16 activations and parameters, groups of 64
+// or 128, in two modes: the reassociated class (rocm_quantized_matmul.
+// gemv_mfma, the default policy's path for tall activations) and, with
+// ROUNDED, the approximate class (rocm_quantized_matmul.mfma: decoded weights
+// rounded to bf16 in the B operand, no group sums or bias term).
 //
 // Counterpart of the reference's matrix paths (metal matrix32 /
 // matrix32_packed, docs/core/quantized-inference.md:138-139,151-170), which
-// decode weights to f32 and are classified "reassociated". Same arithmetic
-// as the decode-batch kernels (gemv_mfma.hip): the packed codes q are exact
-// integers in bf16 MFMA operands, each group's sums sum(x*q) come out of
-// v_mfma_f32_32x32x16_bf16 with f32 accumulation, and the group's scale and
-// bias are applied in f32:
+// decode weights to f32 and are classified "reassociated". In that mode the
+// arithmetic is the decode-batch kernels' (gemv_mfma.hip): the packed codes q
+// are exact integers in bf16 MFMA operands, each group's sums sum(x*q) come
+// out of v_mfma_f32_32x32x16_bf16 with f32 accumulation, and the group's scale
+// and bias are applied in f32:
 //
 //   y = sum_g s_g * sum_{k in g} x_k q_k  +  sum_g b_g * X_g,   X_g = sum_{k in g} x_k.
 //
@@ -21,19 +23,18 @@
 // 3 * 64 / group / 64 of the main loop's matrix work (4.7% at group 64).
 //
 // Work mapping: workgroup tile 256 (rows) x 128 (columns), eight waves in a
-// 4 x 2 arrangement; wave (mi, ni) computes rows 64*mi.. x columns 64*ni..
-// (2 x 2 accumulators of 32 x 32 for y, as many for the current group's
-// sums), two waves per SIMD so that one wave's decode and scaling run on the
-// vector ALU while the other's MFMAs run. K steps of 64; MFMA kk (0..3) of
-// lane half h covers chunk 4h + kk of the step (8 k each), so a lane's codes
-// of one column and step are 16 contiguous bytes.
+// 2 x 4 arrangement (see qgemm_re_kernel), two waves per SIMD so that one
+// wave's decode and scaling run on the vector ALU while the other's MFMAs
+// run. K steps of 64; MFMA kk (0..3) of lane half h covers chunk 4h + kk of
+// the step (8 k each), so a lane's codes of one column and step are 16
+// contiguous bytes.
 //
 // Transfers, all direct global-to-LDS and counted (no compiler-visible loads
-// in the loop): the tile's scales for the whole K range once, first; packed
-// words of four steps at a time (128 bytes per column: whole lines) into two
-// buffers, four steps ahead; activations (256 rows x 128 bytes per step) into
-// a 3-stage ring, two steps ahead. One barrier per step orders the shared
-// tiles.
+// in the loop): the tile's scales (and, ROUNDED, biases) for the whole K
+// range once, first; packed words of four steps at a time (128 bytes per
+// column: whole lines) into two buffers, four steps ahead; activations (256
+// rows x 128 bytes per step) into a 3-stage ring, two steps ahead. One
+// barrier per step orders the shared tiles.
 
 #include "lds_pipeline.h"
 
