@@ -35,6 +35,12 @@ COMMON_FLAGS = [
 # Files whose results must be bit-identical to the CPU oracle: no contraction
 # of a*b+c into a fused multiply-add.
 EXACT_FLAGS = {"quantize.hip": ["-ffp-contract=off"], "generic.hip": ["-ffp-contract=off"]}
+# Decode-batch kernels whose MFMA results feed VALU scaling every step: the
+# MFMAs write ordinary VGPRs, so no accumulator-register read
+# (v_accvgpr_read) sits between each MFMA and its scaling. No kernel in
+# these files needs scratch memory with it.
+VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+UNIT_FLAGS = {**EXACT_FLAGS, **{f: VGPR_MFMA for f in ("gemv_mfma.hip", "vrow_b2.hip", "vrow_b4.hip", "vrow_b8.hip")}}
 
 
 def _sources() -> list[pathlib.Path]:
@@ -43,7 +49,7 @@ def _sources() -> list[pathlib.Path]:
 
 def _compile(source: pathlib.Path) -> pathlib.Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, *EXACT_FLAGS.get(source.name, []), "-c", "-x", "hip", str(source), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *UNIT_FLAGS.get(source.name, []), "-c", "-x", "hip", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stderr}")
