@@ -105,8 +105,15 @@ __device__ __forceinline__ void codes_bf16(const uint32_t* words, u32x4_t* op) {
 // for the step are one contiguous run of 16 and every MFMA stays inside the
 // step. A wave's XROWS activation rows of a step sit in LDS as 16-byte
 // chunks, chunk c of row r at slot c ^ (r%8) ^ ((r/8)%2) (conflict-free
-// fragment reads); with XROWS = 8 the MFMA rows 8..15 repeat rows 0..7 and
-// are not stored.
+// fragment reads).
+//
+// Twin column tiles (XROWS = 8): each stage holds 16 rows, rows 8..15 zero
+// (written once). Fragment "lo" reads rows 0..15 (live rows 0..7), "hi"
+// reads row r ^ 8 (live rows 8..15, holding activation rows 0..7). One
+// MFMA chain then forms column tile 2p against lo and tile 2p+1 against hi,
+// so output rows 0..7 belong to tile 2p and rows 8..15 to tile 2p+1: every
+// output lane carries a live result, and the per-group scaling runs on two
+// accumulators instead of four half-used ones.
 template <int XROWS>
 struct RowBlocks {
   static constexpr int kBlocks = XROWS > 16 ? 2 : 1;  // blocks of 16 MFMA rows
@@ -128,10 +135,14 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   using P = Plan<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst>;
   constexpr int RB = RowBlocks<XROWS>::kBlocks;
   constexpr int kRows = RowBlocks<XROWS>::kRows;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_x[kWaves][kStages][XROWS * 128];
+  constexpr bool kTwin = XROWS == 8;             // twin column tiles
+  constexpr int kLdsRows = kTwin ? 16 : XROWS;   // rows per stage in LDS
+  constexpr int kAcc = kTwin ? 2 : 4;            // accumulators per row block
+  constexpr int kOutRows = kTwin ? 8 : kRows;    // rows with results
+  __shared__ __attribute__((aligned(16))) uint8_t lds_x[kWaves][kStages][kLdsRows * 128];
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[P::kWBufs][kWaves][P::kWBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_p[2][kWaves][P::kPBytes];
-  static_assert(kRows * kCols * 4 <= kStages * XROWS * 128, "partial sums fit in a wave's activation ring");
+  static_assert(kRows * kCols * 4 <= kStages * kLdsRows * 128, "partial sums fit in a wave's activation ring");
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -195,12 +206,14 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
       for (int i = 0; i < P::kWLoads; ++i) ws.issue_w(wstep, i);
     if (!kActsFirst) issue_a(astep);
   };
-  // A operand of MFMA t for row block rb: row 16rb + r (taken mod XROWS when
-  // only 8 rows are staged), chunk 2h + t.
-  auto read_x = [&](int stage, int rb, int t) -> bf16x8_t {
-    const int row = (16 * rb + r) % XROWS;
+  // A operand of MFMA t from LDS row `row`, chunk 2h + t.
+  auto read_row = [&](int stage, int row, int t) -> bf16x8_t {
     const int slot = (2 * h + t) ^ (row & 7) ^ ((row >> 3) & 1);
     return *reinterpret_cast<const bf16x8_t*>(&lds_x[wave][stage][(row >> 3) * 1024 + (8 * (row & 7) + slot) * 16]);
+  };
+  // Row block rb: row 16rb + r; twin tiles: side 0 ("lo") row r, side 1 ("hi") row r ^ 8.
+  auto read_x = [&](int stage, int rb, int t) -> bf16x8_t {
+    return read_row(stage, kTwin ? (r ^ (8 * rb)) : 16 * rb + r, t);
   };
   // The lane's 16 codes of column c (local) for `step`.
   auto read_codes = [&](int step, int c, uint32_t* words) {
@@ -221,11 +234,17 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
 
   const float code_scale = BITS == 8 ? 1.0f : 512.0f;
   const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
-  f32x4_t y[RB][4];
+  f32x4_t y[RB][kAcc];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) y[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int ct = 0; ct < kAcc; ++ct) y[rb][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (kTwin) {  // the zero rows 8..15 of every stage (no transfer writes them)
+#pragma unroll
+    for (int s = 0; s < kStages; ++s)
+      *reinterpret_cast<u32x4_t*>(&lds_x[wave][s][1024 + 16 * lane]) = u32x4_t{0u, 0u, 0u, 0u};
+  }
+  constexpr int kSides = kTwin ? 2 : RB;  // activation fragment sets per step
 
   // Transfers in the order of the transfer plan (Plan<..., kXLoads, PWHOLE,
   // WS>), each wave for itself: iterations -4 .. -1 issue the prologue,
@@ -240,17 +259,16 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
 #define AFFON_QSKINNY_STEP(J)                                                                            \
   {                                                                                                      \
     wait_vmcnt<P::wait_own(J)>();                                                                        \
-    bf16x8_t xf[RB][2];                                                                                  \
-    _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                  \
-      xf[rb][0] = read_x((J), rb, 0);                                                                    \
-      xf[rb][1] = read_x((J), rb, 1);                                                                    \
+    bf16x8_t xf[kSides][2];                                                                              \
+    _Pragma("unroll") for (int sd = 0; sd < kSides; ++sd) {                                              \
+      xf[sd][0] = read_x((J), sd, 0);                                                                    \
+      xf[sd][1] = read_x((J), sd, 1);                                                                    \
     }                                                                                                    \
     uint32_t words[4][BITS];                                                                             \
-    uint32_t s_raw[4], b_raw[4];                                                                         \
-    _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                                   \
-      read_codes(t, 16 * ct + r, words[ct]);                                                             \
-      ws.params(t, 16 * ct + r, 0, &s_raw[ct], &b_raw[ct]);                                              \
-    }                                                                                                    \
+    uint32_t s_raw[kAcc], b_raw[kAcc];                                                                   \
+    _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) read_codes(t, 16 * ct + r, words[ct]);              \
+    _Pragma("unroll") for (int ca = 0; ca < kAcc; ++ca)                                                  \
+      ws.params(t, 16 * (kTwin ? 2 * ca + (h >> 1) : ca) + r, 0, &s_raw[ca], &b_raw[ca]);               \
     wait_lds_reads();                                                                                    \
     issue_all((J), min(t + 4, last & ~3), min(t + P::kWAhead, last & ~(WS - 1)),                         \
               min(t + 3, last));                                                                         \
@@ -258,17 +276,31 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                  \
       xs[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][0], ones, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0); \
       xs[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][1], ones, xs[rb], 0, 0, 0);                \
+      if constexpr (kTwin) {                                                                             \
+        xs[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[1][0], ones, xs[rb], 0, 0, 0);               \
+        xs[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[1][1], ones, xs[rb], 0, 0, 0);               \
+      }                                                                                                  \
     }                                                                                                    \
-    _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                                   \
-      u32x4_t op[2];                                                                                     \
-      codes_bf16<BITS>(words[ct], op);                                                                   \
-      const float sv = widen_param<PT>(s_raw[ct]) * code_scale, bv = widen_param<PT>(b_raw[ct]);         \
+    _Pragma("unroll") for (int ca = 0; ca < kAcc; ++ca) {                                                \
+      const float sv = widen_param<PT>(s_raw[ca]) * code_scale, bv = widen_param<PT>(b_raw[ca]);         \
+      u32x4_t op[2], oq[2];                                                                              \
+      codes_bf16<BITS>(words[kTwin ? 2 * ca : ca], op);                                                  \
+      if constexpr (kTwin) codes_bf16<BITS>(words[2 * ca + 1], oq);                                      \
       _Pragma("unroll") for (int rb = 0; rb < RB; ++rb) {                                                \
-        f32x4_t q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][0], __builtin_bit_cast(bf16x8_t, op[0]), \
-                                                            f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);   \
-        q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][1], __builtin_bit_cast(bf16x8_t, op[1]), q, 0, 0, 0); \
+        f32x4_t q;                                                                                       \
+        if constexpr (kTwin) {                                                                           \
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[0][0], __builtin_bit_cast(bf16x8_t, op[0]),     \
+                                                      f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);         \
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[0][1], __builtin_bit_cast(bf16x8_t, op[1]), q, 0, 0, 0); \
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[1][0], __builtin_bit_cast(bf16x8_t, oq[0]), q, 0, 0, 0); \
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[1][1], __builtin_bit_cast(bf16x8_t, oq[1]), q, 0, 0, 0); \
+        } else {                                                                                         \
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][0], __builtin_bit_cast(bf16x8_t, op[0]),    \
+                                                      f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);         \
+          q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb][1], __builtin_bit_cast(bf16x8_t, op[1]), q, 0, 0, 0); \
+        }                                                                                                \
         _Pragma("unroll") for (int i = 0; i < 4; ++i)                                                    \
-            y[rb][ct][i] = fmaf(sv, q[i], fmaf(bv, xs[rb][i], y[rb][ct][i]));                            \
+            y[rb][ca][i] = fmaf(sv, q[i], fmaf(bv, xs[rb][i], y[rb][ca][i]));                            \
       }                                                                                                  \
     }                                                                                                    \
     ++t;                                                                                                 \
@@ -292,24 +324,29 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   }
 #undef AFFON_QSKINNY_STEP
 
-  // Partial sums of the four K parts, [kRows][kCols] f32 per wave in the
+  // Partial sums of the four K parts, [kOutRows][kCols] f32 per wave in the
   // wave's own activation ring (no transfer into it is in flight any more):
   // output element i of row block rb and column tile ct is row 16rb + 4h + i,
-  // column 16ct + r. Added in wave order.
+  // column 16ct + r; with twin tiles, accumulator ca holds row 4(h%2) + i of
+  // column tile 2ca + h/2. Added in wave order.
   auto ysum = [&](int w) { return reinterpret_cast<float*>(&lds_x[w][0][0]); };
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
+    for (int ca = 0; ca < kAcc; ++ca)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ysum(wave)[(16 * rb + 4 * h + i) * kCols + 16 * ct + r] = y[rb][ct][i];
+      for (int i = 0; i < 4; ++i) {
+        const int row = kTwin ? 4 * (h & 1) + i : 16 * rb + 4 * h + i;
+        const int ct = kTwin ? 2 * ca + (h >> 1) : ca;
+        ysum(wave)[row * kCols + 16 * ct + r] = y[rb][ca][i];
+      }
   __syncthreads();
   float* dst = a.partial + split * static_cast<int64_t>(a.M) * pstride;
   if (a.splits == 1) {
     with_store_kind(a.epi.kind, [&](auto kind) {
       constexpr int KIND = decltype(kind)::value;
 #pragma unroll
-      for (int e = 0; e < kRows * kCols / kThreads; ++e) {
+      for (int e = 0; e < kOutRows * kCols / kThreads; ++e) {
         const int o = e * kThreads + tid;
         const int row = m0 + o / kCols, col = n0 + o % kCols;
         if (row < a.M && col < a.N) {
@@ -320,7 +357,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     });
   } else {
 #pragma unroll
-    for (int e = 0; e < kRows * kCols / kThreads; ++e) {
+    for (int e = 0; e < kOutRows * kCols / kThreads; ++e) {
       const int o = e * kThreads + tid;
       const int row = m0 + o / kCols, col = n0 + o % kCols;
       if (row < a.M && col < a.N)
