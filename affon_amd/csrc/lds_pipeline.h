@@ -198,6 +198,7 @@ struct Plan {
   static_assert(WSTEPS == 1 || WSTEPS == 2 || WSTEPS == 4, "packed-word transfer length");
   static constexpr int kColBytes = 8 * BITS * kStepsPerW;         // bytes per column per transfer
   static constexpr int kSlots = kColBytes / 16;                   // 16-byte slots per column run
+  static_assert(kSlots == 4 || kSlots == 8, "the slot swizzle covers runs of 64 or 128 bytes");
   static constexpr int kWLoads = 64 * kColBytes / 1024;           // 16-byte DMA instructions per transfer
   static constexpr int kWBytes = 64 * kColBytes;                  // per wave and buffer
   static constexpr int kWBufs = kStepsPerW == 1 ? kStages : 2;    // ring depth (buffers)
