@@ -10,8 +10,9 @@
 // step sums: y += s * sum(x*q) + b * sum(x) -- the arithmetic of the VALU
 // decode kernel, with sum(x) from one more MFMA against a bf16 ones operand.
 //
-// Work mapping: a (16 or 32) x 64 tile per workgroup (rows past M repeat row
-// M-1 and are not stored), its four waves each on a quarter of the K range, K
+// Work mapping: an (8, 16 or 32) x 64 tile per workgroup (rows past M repeat
+// row M-1 and are not stored; at 8 rows the MFMA's other 8 rows carry a
+// second column tile), its four waves each on a quarter of the K range, K
 // split further over workgroups when the tiles alone cannot fill the GPU.
 // Operands reach LDS by the same direct transfers, ring and counted waits as
 // the prefill GEMM (lds_pipeline.h).
