@@ -525,8 +525,8 @@ def test_gemv_mfma_selected_for_decode_batches(session):
 
 def test_prefill_split_k_deterministic(session):
     """Shapes with few tiles split K over workgroups (partials summed in range
-    order by the last arrival): repeated runs are bit-identical, and match the
-    reassociated decode kernel within the bf16 tolerance."""
+    order by the reduction kernel): repeated runs are bit-identical, and match
+    the reassociated decode kernel within the bf16 tolerance."""
     for M, N, K, bits, group in [(512, 4096, 14336, 4, 64), (64, 256, 4096, 8, 64), (300, 300, 1024, 2, 128)]:
         x, packed, s, b = seeded_problem(M, N, K, bits, group, "bf16", "bf16", seed=11)
         xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
