@@ -38,6 +38,8 @@ CASES = [
     (2, 136, 1024, 8, 64, "bf16", "bf16"),
     (4, 72, 512, 4, 32, "bf16", "f32"),
     (16, 128, 1024, 4, 64, "bf16", "bf16"),
+    (8, 200, 2048, 4, 64, "bf16", "bf16"),  # LDS-tiled kernel with twin column tiles (split K)
+    (6, 136, 4096, 8, 128, "bf16", "f32"),  # the same, 8-bit codes and f32 parameters
     (3, 77, 256, 2, 64, "f32", "bf16"),
     (64, 192, 512, 4, 64, "bf16", "bf16"),
     (96, 64, 4096, 8, 128, "bf16", "bf16"),
@@ -219,13 +221,14 @@ def test_epilogue_validation_leaves_output_untouched(session):
                                                         ("bf16", "bf16", 8, 32)])
 @pytest.mark.parametrize("sizes", [(4096, 1024, 1024), (300, 77, 13, 8)], ids=["qkv", "ragged"])
 def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, group, sizes, rng):
-    """Projections of one input in one launch (M = 1: the gemv kernel; M = 16
-    with bf16 activations: the LDS-tiled gemv_mfma kernel, whose split-K
-    partials span all projections) or in sequence (M = 2), with output biases
+    """Projections of one input in one launch (M = 1: the gemv kernel; M = 8
+    and 16 with bf16 activations: the LDS-tiled gemv_mfma kernel, at 8 rows
+    with twin column tiles, whose split-K partials span all projections) or
+    in sequence (M = 2), with output biases
     on some of them; ragged sizes exercise the padding between projections.
     Group 32 at 4 and 8 bits takes the M=1 kernel's per-lane parameter loads."""
     K = 1024
-    for M in (1, 2, 16):
+    for M in (1, 2, 8, 16):
         projections, host = [], []
         x = seeded_problem(M, 8, K, bits, group, x_dtype, p_dtype, seed=59)[0]
         for i, n in enumerate(sizes):
@@ -239,7 +242,7 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, gro
             host.append((packed, s, b, bias))
         xt = upload(session, x, dtype_of(x))
         plan = A.grouped_plan(xt, projections, bits=bits, group_size=group)
-        one_launch = M == 1 or (M == 16 and x_dtype == "bf16" and group % 64 == 0)  # tiled: K steps of 64
+        one_launch = M == 1 or (M in (8, 16) and x_dtype == "bf16" and group % 64 == 0)  # tiled: K steps of 64
         if one_launch:
             kernel = "gemv" if M == 1 else "gemv_mfma"
             assert plan == f"rocm_quantized_matmul.{kernel}[grouped:{len(sizes)},bias]", plan
