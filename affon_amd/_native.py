@@ -62,6 +62,16 @@ class Epilogue(ctypes.Structure):
     ]
 
 
+class FloorGeometry(ctypes.Structure):
+    """affon_rocm_floor_geometry: one read-floor launch shape."""
+    _fields_ = [
+        ("kib_per_wave", c_int32),
+        ("threads", c_int32),
+        ("valu_per_wave", c_int32),
+        ("store_every", c_int32),
+    ]
+
+
 SIGNATURES = {
     "affon_rocm_device_count": (c_int, [ctypes.POINTER(c_int)]),
     "affon_rocm_session_create": (c_int, [c_int, ctypes.POINTER(c_void_p)]),
@@ -78,6 +88,9 @@ SIGNATURES = {
     "affon_rocm_quantized_matmul_noalloc": (c_int, [c_void_p, ctypes.POINTER(QmmDesc)]),
     "affon_rocm_read_floor": (c_int, [c_void_p, ctypes.POINTER(c_void_p), ctypes.POINTER(ctypes.c_uint64), c_int,
                                       c_void_p]),
+    "affon_rocm_read_floor_geometry": (c_int, [c_void_p, c_void_p, ctypes.c_uint64, c_void_p, ctypes.c_uint64,
+                                               ctypes.POINTER(FloorGeometry)]),
+    "affon_rocm_empty_launch": (c_int, [c_void_p, c_uint32, c_uint32]),
     "affon_rocm_quantized_matmul_select": (c_int, [ctypes.POINTER(QmmDesc), c_char_p, c_size_t]),
     "affon_rocm_quantized_matmul_fused": (c_int, [c_void_p, ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue)]),
     "affon_rocm_quantized_matmul_fused_select": (c_int, [ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue), c_char_p,

@@ -479,6 +479,46 @@ int affon_rocm_read_floor(affon_rocm_session* session, const void* const* buffer
   return AFFON_ROCM_OK;
 }
 
+int affon_rocm_read_floor_geometry(affon_rocm_session* session, const void* buffer, uint64_t bytes, void* sink,
+                                   uint64_t sink_bytes, const affon_rocm_floor_geometry* geometry) {
+  clear_error();
+  if (geometry == nullptr || buffer == nullptr || sink == nullptr)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry needs a buffer, a sink and a geometry");
+  const affon_rocm_floor_geometry g = *geometry;
+  if (reinterpret_cast<uintptr_t>(buffer) % 16 != 0 || reinterpret_cast<uintptr_t>(sink) % 8 != 0 || bytes < 16 ||
+      bytes % 16 != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry: buffer unaligned, or bytes not a positive multiple of 16");
+  if (g.kib_per_wave != 1 && g.kib_per_wave != 2 && g.kib_per_wave != 4 && g.kib_per_wave != 8)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry: kib_per_wave must be 1, 2, 4 or 8");
+  if (g.threads < 64 || g.threads > 1024 || g.threads % 64 != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry: threads must be a multiple of 64 from 64 to 1024");
+  if (g.valu_per_wave < 0 || g.valu_per_wave > 4096 || g.valu_per_wave % 8 != 0)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry: valu_per_wave must be a multiple of 8 from 0 to 4096");
+  if (g.store_every < 0) return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry: store_every must be >= 0");
+  const uint64_t waves = affon::read_geometry_waves(bytes, g.kib_per_wave);
+  const uint64_t need = g.store_every > 0 ? 8 * ((waves + g.store_every - 1) / g.store_every) : 4;
+  if (sink_bytes < need)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "read_floor_geometry: sink holds %llu bytes, the stores need %llu",
+                static_cast<unsigned long long>(sink_bytes), static_cast<unsigned long long>(need));
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::read_geometry_launch(buffer, bytes, static_cast<float*>(sink), g.kib_per_wave, g.threads,
+                                             g.store_every, g.valu_per_wave, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "read_floor_geometry");
+  return AFFON_ROCM_OK;
+}
+
+int affon_rocm_empty_launch(affon_rocm_session* session, uint32_t blocks, uint32_t threads) {
+  clear_error();
+  if (blocks < 1 || blocks > 0x7fffffffu || threads < 1 || threads > 1024)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "empty_launch: 1 to 2^31-1 workgroups of 1 to 1024 threads");
+  int status = check_session(session);
+  if (status != AFFON_ROCM_OK) return status;
+  hipError_t e = affon::empty_launch(blocks, threads, session->stream);
+  if (e != hipSuccess) return hip_fail(e, "empty_launch");
+  return AFFON_ROCM_OK;
+}
+
 int affon_rocm_quantized_matmul_select(const affon_rocm_qmm_desc* desc, char* id, size_t cap) {
   clear_error();
   affon::QmmProblem p;

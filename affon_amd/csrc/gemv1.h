@@ -156,22 +156,27 @@ __device__ __forceinline__ bf16x2_t pack2(float a, float b) { return bf16x2_t{st
 // 4-bit and 2-bit codes: a byte holding a code n < 16 read as an FP8 E4M3
 // value is exactly n * 2^-9 (the subnormal range and the first binade of E4M3
 // are evenly spaced by 2^-9), so one v_cvt_scalef32_pk_bf16_fp8 (bf16) or
-// v_cvt_pk_f32_fp8 (f32) turns two codes into exact operands. The unit is
-// measured in the kernel (fp8_unit) rather than assumed, and divided out of the
-// group scale. 8-bit codes use v_cvt_f32_ubyteN (one exact conversion each).
+// v_cvt_scalef32_pk_f32_fp8 (f32) turns two codes into exact operands. The
+// unit is measured in the kernel (fp8_unit) rather than assumed, and the
+// conversions scale by its reciprocal (a power of two), so they return the
+// codes themselves. 8-bit codes use v_cvt_f32_ubyteN (one exact conversion
+// each).
 //
 // Operand order: bf16 activations are staged in LDS in the pair order the
 // conversions produce (see stage_chunk), f32 activations in k order.
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ bf16x2_t fp8_pair_bf16(uint32_t bytes, bool high) {
-  return high ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, 1.0f, true)
-              : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, 1.0f, false);
+// `scale` multiplies the converted values; a power of two keeps them exact
+// (the kernel passes 1 / unit, so the codes come out as integers).
+__device__ __forceinline__ bf16x2_t fp8_pair_bf16(uint32_t bytes, bool high, float scale = 1.0f) {
+  return high ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, scale, true)
+              : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(bytes, scale, false);
 }
 
-__device__ __forceinline__ f32x2_t fp8_pair_f32(uint32_t bytes, bool high) {
-  return high ? __builtin_amdgcn_cvt_pk_f32_fp8(bytes, true) : __builtin_amdgcn_cvt_pk_f32_fp8(bytes, false);
+__device__ __forceinline__ f32x2_t fp8_pair_f32(uint32_t bytes, bool high, float scale = 1.0f) {
+  return high ? __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bytes, scale, true)
+              : __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bytes, scale, false);
 }
 
 // Value of one code step after the FP8 conversion (2^-9 for OCP E4M3).
@@ -214,11 +219,13 @@ __device__ __forceinline__ int pair_slot(int i, int t, int h) {
   return BITS == 4 ? i * 4 + 2 * t + h : i * 8 + 4 * h + t;
 }
 
-// Sum over one 16-byte chunk (4 words) of x*q in units of the code step
-// (fp8 path) or exactly (8-bit path). xr holds the chunk's activations as
-// staged: bf16 pairs, or f32 values in k order.
+// Sum over one 16-byte chunk (4 words) of x*q, exactly in the codes: the fp8
+// conversions of 2/4-bit codes take `scale` = 1 / unit (a power of two, so
+// the converted codes are the integers themselves); 8-bit codes convert
+// directly. xr holds the chunk's activations as staged: bf16 pairs, or f32
+// values in k order.
 template <int BITS, typename XT>
-__device__ __forceinline__ float chunk_dot(const uint32_t* words, const uint32_t* xr) {
+__device__ __forceinline__ float chunk_dot(const uint32_t* words, const uint32_t* xr, float scale = 1.0f) {
   constexpr int P = 32 / BITS;
   float acc = 0.0f;
 #pragma unroll
@@ -246,11 +253,11 @@ __device__ __forceinline__ float chunk_dot(const uint32_t* words, const uint32_t
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           if constexpr (XT::bytes == 2) {
-            acc = __builtin_amdgcn_fdot2_f32_bf16(fp8_pair_bf16(m, h == 1),
+            acc = __builtin_amdgcn_fdot2_f32_bf16(fp8_pair_bf16(m, h == 1, scale),
                                                   __builtin_bit_cast(bf16x2_t, xr[pair_slot<BITS>(i, t, h)]), acc,
                                                   false);
           } else {
-            const f32x2_t q = fp8_pair_f32(m, h == 1);
+            const f32x2_t q = fp8_pair_f32(m, h == 1, scale);
             acc = fmaf(__uint_as_float(xr[i * P + code_k<BITS>(t, 2 * h)]), q.x, acc);
             acc = fmaf(__uint_as_float(xr[i * P + code_k<BITS>(t, 2 * h + 1)]), q.y, acc);
           }
@@ -492,9 +499,9 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
       const int64_t n = row_of(r);
       const uint8_t* srow = (second(r) ? a.epi.s2 : S) + n * a.ss0 * PT::bytes;
       const uint8_t* brow = (second(r) ? a.epi.b2 : B) + n * a.bs0 * PT::bytes;
-      if constexpr (PT::bytes == 2) {
-        sraw[r][i] = *reinterpret_cast<const uint16_t*>(srow + goff);
-        braw[r][i] = *reinterpret_cast<const uint16_t*>(brow + goff);
+      if constexpr (PT::bytes == 2) {  // widened to f32 bits once per load
+        sraw[r][i] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(srow + goff)) << 16;
+        braw[r][i] = static_cast<uint32_t>(*reinterpret_cast<const uint16_t*>(brow + goff)) << 16;
       } else {
         sraw[r][i] = *reinterpret_cast<const uint32_t*>(srow + goff);
         braw[r][i] = *reinterpret_cast<const uint32_t*>(brow + goff);
@@ -537,11 +544,12 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
   }
   __syncthreads();
 
-  // 3. Decode, multiply, apply group parameters per chunk.
-  // Converted codes are n * unit; scales are divided by the unit (a power of
-  // two, so exactly).
-  const float inv_unit = BITS == 8 ? 1.0f : pow2_reciprocal(fp8_unit<XT>());
-  auto param = [](uint32_t raw) { return __uint_as_float(PT::bytes == 2 ? raw << 16 : raw); };
+  // 3. Decode, multiply, apply group parameters per chunk. The fp8
+  // conversions read a code n as n * unit; scaling them by 1 / unit (a power
+  // of two, uniform across the wave) makes the converted codes exact integers.
+  const float code_scale =
+      BITS == 8 ? 1.0f : __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pow2_reciprocal(fp8_unit<XT>()))));
+  auto param = [](uint32_t bits) { return __uint_as_float(bits); };
   float y[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) y[r] = 0.0f;
@@ -561,8 +569,8 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
       const float xsum = xsum_lds[c];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float acc = chunk_dot<BITS, XT>(wv[r][i], xr);
-        y[r] = fmaf(param(param_of<LG>(sraw[r], i)) * inv_unit, acc, fmaf(param(param_of<LG>(braw[r], i)), xsum, y[r]));
+        const float acc = chunk_dot<BITS, XT>(wv[r][i], xr, code_scale);
+        y[r] = fmaf(param(param_of<LG>(sraw[r], i)), acc, fmaf(param(param_of<LG>(braw[r], i)), xsum, y[r]));
       }
     }
   }

@@ -134,6 +134,11 @@ hipError_t index_select_launch(const void* x, int dtype, int64_t rows, int64_t c
 // (diag.hip); sink receives at most one word.
 hipError_t read_floor_launch(const void* const* buffers, const uint64_t* bytes, int count, uint32_t* sink,
                              hipStream_t stream);
+// Geometry sweep of the read floor and an empty launch (diag.hip).
+hipError_t read_geometry_launch(const void* buffer, uint64_t bytes, float* sink, int kib_per_wave, int threads,
+                                int store_every, int valu_per_wave, hipStream_t stream);
+uint64_t read_geometry_waves(uint64_t bytes, int kib_per_wave);
+hipError_t empty_launch(unsigned blocks, unsigned threads, hipStream_t stream);
 hipError_t dequantize_launch(const uint32_t* packed, const void* scales, const void* biases,
                              int param_dtype, int64_t rows, int64_t columns, int bits, int64_t group,
                              void* out, int out_dtype, hipStream_t stream);

@@ -448,6 +448,126 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
             "TFLOP/s": round(flops / (t * 1e-3) / 1e12, 3), "algorithmic_bytes": nbytes, "weight_sets": sets}
 
 
+def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
+    """Per-launch milliseconds of `steps` launches captured in one HIP graph
+    on the session stream, for each of REPLAYS replays (after `warmup`
+    direct launches and one untimed replay). launch(i) enqueues launch i."""
+    stream = ctypes.c_void_p(session.stream)
+    for i in range(warmup):
+        launch(i)
+    session.synchronize()
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+    for i in range(steps):
+        launch(i)
+    hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+    hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+    hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+    session.synchronize()
+    start, stop = hip.event(), hip.event()
+    runs = []
+    for _ in range(REPLAYS):
+        hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+        hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+        hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+        hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+        runs.append(ms.value / steps)
+    hip.lib.hipGraphExecDestroy(exe)
+    hip.lib.hipGraphDestroy(graph)
+    hip.lib.hipEventDestroy(start)
+    hip.lib.hipEventDestroy(stop)
+    return runs
+
+
+def median(values):
+    return sorted(values)[len(values) // 2]
+
+
+def floor_sweep(session, hip: Hip, steps: int, warmup: int) -> dict:
+    """What a decode launch's graph-replay period is made of, measured with
+    the library's diagnostic kernels over rotated random data (never a MALL
+    hit): the period of an empty launch; pure reads of the 4-bit 14336 x 4096
+    weight set (33,095,680 bytes) by read geometry (KiB per wave, workgroup
+    size); the same reads plus output stores (by how many waves store) and
+    plus vector arithmetic per wave (the M = 1 decode's packed-word
+    arithmetic alone is 88 instructions per 2 KiB); pure reads by size (a
+    stream rate plus a fixed cost); and the decode kernel itself against the
+    number of weight rows, fitted the same way."""
+    from affon_amd import _native
+    lib = _native.load()
+    progress = lambda m: print(f"floor-sweep: {m}", file=sys.stderr, flush=True)  # noqa: E731
+    pool_bytes = 1200 << 20
+    pool = session.empty("u32", (pool_bytes // 4,))
+    rng = np.random.default_rng(7)
+    piece = rng.integers(0, 2**32, size=(64 << 20) // 4, dtype=np.uint32)
+    for off in range(0, pool_bytes, piece.nbytes):
+        piece ^= np.uint32(0x9E3779B9)
+        _native.check(lib.affon_rocm_memcpy_h2d(session._handle, pool.data_ptr + off, piece.ctypes.data,
+                                                min(piece.nbytes, pool_bytes - off)), "upload")
+    sink = session.empty("u32", (1 << 20,))
+    headline = 33095680
+    out = {"headline_bytes": headline, "pool_bytes": pool_bytes, "steps": steps}
+
+    def offsets(nbytes):
+        stride = (nbytes + 4095) // 4096 * 4096
+        return [pool.data_ptr + k * stride for k in range(pool_bytes // stride)]
+
+    def read(nbytes, kib=2, threads=256, valu=0, store_every=0):
+        ptrs = offsets(nbytes)
+        g = _native.FloorGeometry(kib, threads, valu, store_every)
+
+        def launch(i):
+            _native.check(lib.affon_rocm_read_floor_geometry(session._handle, ptrs[i % len(ptrs)], nbytes,
+                                                             sink.data_ptr, sink._buffer.nbytes, ctypes.byref(g)),
+                          "read_floor_geometry")
+        return round(median(time_graph(hip, session, launch, steps, warmup)) * 1e3, 3)
+
+    def empty(blocks, threads):
+        def launch(i):
+            _native.check(lib.affon_rocm_empty_launch(session._handle, blocks, threads), "empty_launch")
+        return round(median(time_graph(hip, session, launch, steps, warmup)) * 1e3, 3)
+
+    out["empty_launch_us"] = {"1x64": empty(1, 64), "1792x256": empty(1792, 256), "7168x256": empty(7168, 256)}
+    progress(f"empty launch {out['empty_launch_us']}")
+    geometry = {}
+    for kib in (1, 2, 4, 8):
+        for threads in (64, 128, 256, 512, 1024):
+            geometry[f"{kib}KiB_per_wave_T{threads}"] = read(headline, kib, threads)
+    out["read_us_by_geometry"] = geometry
+    best = min(geometry, key=geometry.get)
+    out["best_read"] = {"geometry": best, "us": geometry[best],
+                        "GB/s": round(headline / (geometry[best] * 1e-6) / 1e9, 1)}
+    progress(f"best read geometry {out['best_read']}")
+    out["read_us_by_store_every"] = {str(e): read(headline, 2, 256, 0, e) for e in (0, 1, 4, 16, 64)}
+    out["read_us_by_valu_per_wave"] = {str(v): read(headline, 2, 256, v) for v in (0, 32, 64, 88, 128, 176, 256, 352)}
+    progress(f"stores {out['read_us_by_store_every']}; arithmetic {out['read_us_by_valu_per_wave']}")
+    sizes = {}
+    for mb in (4, 8, 16, 32, 64, 128, 296):
+        nbytes = mb << 20
+        sizes[str(nbytes)] = read(nbytes, 2, 256)
+    out["read_us_by_bytes"] = sizes
+    xs = np.array([float(b) for b in sizes]), np.array(list(sizes.values()))
+    slope, fixed = np.polyfit(xs[0], xs[1], 1)
+    out["read_fit"] = {"fixed_us": round(float(fixed), 3), "stream_GB/s": round(1e-3 / float(slope), 1)}
+    progress(f"read fit {out['read_fit']}")
+    pool.dispose()
+    pool = None  # the allocation is freed with its last reference
+    decode = {}
+    for N in (1792, 3584, 7168, 14336, 28672, 57344, 128256):
+        work = Workload(session, f"decode_4bit_g64_m1_n{N}", 1, N, 4096, 4, 64)
+        decode[str(N)] = {"bytes": work.bytes, "us": round(work.time(hip, steps, warmup) * 1e3, 3),
+                          "implementation": work.implementation}
+        work.release()
+        progress(f"decode N={N}: {decode[str(N)]['us']} us")
+    out["decode_us_by_rows"] = decode
+    xs = np.array([v["bytes"] for v in decode.values()], dtype=float), np.array([v["us"] for v in decode.values()])
+    slope, fixed = np.polyfit(xs[0], xs[1], 1)
+    out["decode_fit"] = {"fixed_us": round(float(fixed), 3), "stream_GB/s": round(1e-3 / float(slope), 1)}
+    return out
+
+
 def copy_calibration(session) -> int:
     """Copies of a known size, profiled with the same byte counters as the
     kernels, give the factor from counter units to bytes."""
@@ -473,6 +593,8 @@ def main() -> int:
     parser.add_argument("--only", default="", help="comma-separated subset of extra workloads to run ('none': no extras)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 8 device-to-device copies of 256 MiB (for scaling hardware byte counters)")
+    parser.add_argument("--floor-sweep", action="store_true",
+                        help="only measure what an M = 1 decode launch's period is made of (prints one JSON line)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the quantized linear path has no multi-GPU execution "
@@ -485,6 +607,10 @@ def main() -> int:
     use_graph = args.launch == "graph"
     if args.copy_calibration:
         return copy_calibration(session)
+    if args.floor_sweep:
+        print(json.dumps({"floor_sweep": floor_sweep(session, hip, args.steps, args.warmup)}), flush=True)
+        session.dispose()
+        return 0
 
     def progress(message: str) -> None:
         print(f"bench: {message}", file=sys.stderr, flush=True)

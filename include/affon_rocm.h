@@ -147,6 +147,27 @@ int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon
 int affon_rocm_read_floor(affon_rocm_session* session, const void* const* buffers, const uint64_t* bytes, int count,
                           void* sink);
 
+/* Measurement helpers, no counterpart in the reference: the parts a decode
+ * launch's period is made of. affon_rocm_read_floor_geometry reads `bytes`
+ * (a multiple of 16) of one 16-byte-aligned device buffer once: every wave
+ * reads `kib_per_wave` (1, 2, 4 or 8) contiguous KiB with one 16-byte load per
+ * lane per KiB, all issued before any wait, in workgroups of `threads` (64 to
+ * 1024, a multiple of 64); then issues `valu_per_wave` (a multiple of 8, at
+ * most 4096) dependent f32 multiply-adds on its data; then, when
+ * `store_every` > 0, every store_every-th wave writes 8 bytes to `sink`,
+ * which must hold 8 * ceil(waves / store_every) bytes (sink_bytes; waves =
+ * ceil(bytes / (1024 * kib_per_wave))). affon_rocm_empty_launch enqueues a
+ * kernel that does nothing, on `blocks` workgroups of `threads`. */
+typedef struct {
+  int32_t kib_per_wave;
+  int32_t threads;
+  int32_t valu_per_wave;
+  int32_t store_every;
+} affon_rocm_floor_geometry;
+int affon_rocm_read_floor_geometry(affon_rocm_session* session, const void* buffer, uint64_t bytes, void* sink,
+                                   uint64_t sink_bytes, const affon_rocm_floor_geometry* geometry);
+int affon_rocm_empty_launch(affon_rocm_session* session, uint32_t blocks, uint32_t threads);
+
 /* Runs validation and selection only and writes the selected implementation
  * id (e.g. "rocm_quantized_matmul.gemv") into id (capacity cap, NUL-terminated).
  * Mirrors the compiler's implementation_id in executable explanations
