@@ -91,6 +91,7 @@ SIGNATURES = {
     "affon_rocm_read_floor_geometry": (c_int, [c_void_p, c_void_p, ctypes.c_uint64, c_void_p, ctypes.c_uint64,
                                                ctypes.POINTER(FloorGeometry)]),
     "affon_rocm_empty_launch": (c_int, [c_void_p, c_uint32, c_uint32]),
+    "affon_rocm_kernel_supports": (c_int, [ctypes.POINTER(QmmDesc), c_char_p, ctypes.POINTER(c_int)]),
     "affon_rocm_quantized_matmul_select": (c_int, [ctypes.POINTER(QmmDesc), c_char_p, c_size_t]),
     "affon_rocm_quantized_matmul_fused": (c_int, [c_void_p, ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue)]),
     "affon_rocm_quantized_matmul_fused_select": (c_int, [ctypes.POINTER(QmmDesc), ctypes.POINTER(Epilogue), c_char_p,

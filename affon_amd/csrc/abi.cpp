@@ -26,6 +26,9 @@ struct affon_rocm_session {
   affon::Workspace* workspace = nullptr;
   // Allocations made through affon_rocm_alloc and not yet freed: the
   // session frees them when it ends, so tensors that outlive it leak nothing.
+  // alloc and free may come from any thread (a caller's garbage collector
+  // frees from whichever thread it runs on): the mutex guards the set.
+  std::mutex allocations_mutex;
   std::unordered_set<void*> allocations;
 };
 
@@ -70,36 +73,36 @@ void* Workspace::get(size_t bytes) {
 }  // namespace affon
 
 // Scratch memory of affon_rocm_quantized_matmul_noalloc: the split-K partial
-// sums of the tiled kernels, in a static device array (one per GPU, held
-// until the process ends). Host code uses only the per-device address that
-// hipGetSymbolAddress returns for it (kept by scratch_on), never the array's
-// name, which on the host is a stand-in and not a device address.
-constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+// sums of the tiled kernels and the reassociated prefill GEMM's per-group
+// activation sums, in a static device array (one per GPU, held until the
+// process ends): 32 MiB of partial sums (four K ranges of a 512 x 4096 f32
+// output) plus 1 MiB of group sums. Host code uses only the per-device
+// address that hipGetSymbolAddress returns for it (kept by scratch_on), never
+// the array's name, which on the host is a stand-in and not a device address.
+constexpr size_t kNoAllocScratchBytes = (size_t(32) << 20) + (size_t(1) << 20);
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace {
 
-// Device address of `scratch` on `device`, looked up once per device with the
-// device current (at session creation); nullptr when the lookup failed.
+// Device address of `scratch` on `device`, looked up on the first
+// no-allocation call on that device, with the device current (check_session
+// has made it so); only a successful lookup is kept, so a failed one is
+// retried by the next call.
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[64] = {};
-bool g_scratch_done[64] = {};
 
-hipError_t scratch_setup(int device) {
+hipError_t scratch_on(int device, void** out) {
+  *out = nullptr;
   if (device < 0 || device >= 64) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  if (g_scratch_done[device]) return g_scratch_ptr[device] != nullptr ? hipSuccess : hipErrorInvalidSymbol;
-  void* ptr = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-  g_scratch_done[device] = true;
-  g_scratch_ptr[device] = e == hipSuccess ? ptr : nullptr;
-  return e;
-}
-
-void* scratch_on(int device) {
-  if (device < 0 || device >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  return g_scratch_ptr[device];
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return hipSuccess;
 }
 
 thread_local std::string g_last_error;
@@ -325,11 +328,6 @@ int affon_rocm_session_create(int device, affon_rocm_session** out) {
   if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
   hipStream_t stream = nullptr;
   if ((e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)) != hipSuccess) return hip_fail(e, "hipStreamCreate");
-  // The no-allocation entry point's scratch address on this device.
-  if ((e = scratch_setup(device)) != hipSuccess) {
-    (void)hipStreamDestroy(stream);
-    return hip_fail(e, "hipGetSymbolAddress(scratch)");
-  }
   auto* session = new affon_rocm_session;
   session->device = device;
   session->stream = stream;
@@ -345,7 +343,11 @@ int affon_rocm_session_destroy(affon_rocm_session* session) {
   if (hipSetDevice(session->device) == hipSuccess && session->stream != nullptr) {
     hipError_t e = hipStreamSynchronize(session->stream);
     if (e != hipSuccess) status = hip_fail(e, "hipStreamSynchronize");
-    for (void* ptr : session->allocations) (void)hipFree(ptr);
+    {
+      std::lock_guard<std::mutex> lock(session->allocations_mutex);
+      for (void* ptr : session->allocations) (void)hipFree(ptr);
+      session->allocations.clear();
+    }
     delete session->workspace;
     e = hipStreamDestroy(session->stream);
     if (e != hipSuccess && status == AFFON_ROCM_OK) status = hip_fail(e, "hipStreamDestroy");
@@ -368,6 +370,7 @@ int affon_rocm_alloc(affon_rocm_session* session, size_t bytes, void** out) {
   *out = nullptr;
   hipError_t e = hipMalloc(out, bytes == 0 ? 1 : bytes);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  std::lock_guard<std::mutex> lock(session->allocations_mutex);
   session->allocations.insert(*out);
   return AFFON_ROCM_OK;
 }
@@ -377,8 +380,11 @@ int affon_rocm_free(affon_rocm_session* session, void* ptr) {
   int status = check_session(session);
   if (status != AFFON_ROCM_OK) return status;
   if (ptr == nullptr) return AFFON_ROCM_OK;
-  if (session->allocations.erase(ptr) == 0)
-    return fail(AFFON_ROCM_CORE_FAILURE, "free of memory this session did not allocate");
+  {
+    std::lock_guard<std::mutex> lock(session->allocations_mutex);
+    if (session->allocations.erase(ptr) == 0)
+      return fail(AFFON_ROCM_CORE_FAILURE, "free of memory this session did not allocate");
+  }
   hipError_t e = hipStreamSynchronize(session->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   e = hipFree(ptr);
@@ -446,9 +452,9 @@ int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon
   const Candidate* c = nullptr;
   if ((status = select(desc, p, &c)) != AFFON_ROCM_OK) return status;
   if ((status = check_session(session)) != AFFON_ROCM_OK) return status;
-  void* fixed = scratch_on(session->device);
-  if (fixed == nullptr) return fail(AFFON_ROCM_CORE_FAILURE, "no-allocation scratch is not set up on device %d",
-                                    session->device);
+  void* fixed = nullptr;
+  if (hipError_t e = scratch_on(session->device, &fixed); e != hipSuccess)
+    return hip_fail(e, "hipGetSymbolAddress(scratch)");
   affon::Launch launch;
   launch.stream = session->stream;
   launch.fixed = fixed;
@@ -517,6 +523,30 @@ int affon_rocm_empty_launch(affon_rocm_session* session, uint32_t blocks, uint32
   hipError_t e = affon::empty_launch(blocks, threads, session->stream);
   if (e != hipSuccess) return hip_fail(e, "empty_launch");
   return AFFON_ROCM_OK;
+}
+
+int affon_rocm_kernel_supports(const affon_rocm_qmm_desc* desc, const char* kernel, int* supported) {
+  clear_error();
+  if (kernel == nullptr || supported == nullptr)
+    return fail(AFFON_ROCM_INVALID_SHAPE, "kernel_supports needs a kernel name and a result pointer");
+  affon::QmmProblem p;
+  int status = validate(desc, &p);
+  if (status != AFFON_ROCM_OK) return status;
+  static const struct {
+    const char* name;
+    bool (*guard)(const affon::QmmProblem&);
+  } kGuards[] = {
+      {"generic", affon::generic_supports}, {"gemv", affon::gemv_supports},     {"gemv1", affon::gemv1_supports},
+      {"gemv_mfma", affon::gemv_mfma_supports}, {"mfma", affon::mfma_supports}, {"gemm_re", affon::re_gemm_supports},
+      {"gemm_pair", affon::pair_supports},
+  };
+  for (const auto& g : kGuards) {
+    if (std::strcmp(g.name, kernel) == 0) {
+      *supported = g.guard(p) ? 1 : 0;
+      return AFFON_ROCM_OK;
+    }
+  }
+  return fail(AFFON_ROCM_INVALID_SHAPE, "kernel_supports: unknown kernel '%s'", kernel);
 }
 
 int affon_rocm_quantized_matmul_select(const affon_rocm_qmm_desc* desc, char* id, size_t cap) {

@@ -540,6 +540,14 @@ bool re_gemm_supports(const QmmProblem& p) {
   if (reinterpret_cast<uintptr_t>(p.s) % 4 != 0 || reinterpret_cast<uintptr_t>(p.b) % 4 != 0) return false;
   if (p.ss0 % 2 != 0 || p.bs0 % 2 != 0) return false;
   if (p.M > (int64_t(1) << 24) || p.N > (int64_t(1) << 20) || p.K > (int64_t(1) << 24)) return false;
+  // The transfers take 32-bit lane offsets from a scalar base: the row of
+  // the last activation row and the column of the last weight column, in
+  // bytes, stay below 2^31 (as the parameter rows, read with 64-bit offsets,
+  // do for symmetry); the grid (tiles x at most 8 K ranges) stays an int.
+  const int64_t limit = int64_t(1) << 31;
+  if (p.M * p.xs0 * 2 >= limit || p.N * p.ws0 * 4 >= limit) return false;
+  if (p.N * p.ss0 * 2 >= limit || p.N * p.bs0 * 2 >= limit) return false;
+  if (((p.N + kCols - 1) / kCols) * ((p.M + kRows - 1) / kRows) > (int64_t(1) << 27)) return false;
   return true;
 }
 
@@ -561,7 +569,14 @@ bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status, bo
   const size_t total = ((partial_bytes + 255) & ~size_t(255)) + plane_bytes;
   uint8_t* scratch = nullptr;
   if (total > 0) {
-    if (l.fixed != nullptr && total > l.fixed_bytes) return false;  // the caller's other path runs instead
+    if (l.fixed != nullptr && total > l.fixed_bytes) {
+      // A fixed buffer too small for this plan: nothing is launched and the
+      // caller rejects the shape (running another kernel would change the
+      // plan the allocating entry point runs).
+      l.fixed_short = total;
+      *status = hipErrorOutOfMemory;
+      return true;
+    }
     if (!l.can_split() || (scratch = static_cast<uint8_t*>(l.scratch(total))) == nullptr) return false;
   }
 

@@ -84,6 +84,8 @@ bool generic_supports(const QmmProblem& p);
 hipError_t generic_launch(const QmmProblem& p, const Launch& l);
 
 bool gemv_supports(const QmmProblem& p);
+// The M = 1 kernel of the gemv candidate (gemv1.h).
+bool gemv1_supports(const QmmProblem& p);
 // Whether the gemv candidate computes a kSiluPair problem (both projections)
 // in one launch.
 bool gemv_pair_supports(const QmmProblem& p);

@@ -127,13 +127,14 @@ int affon_rocm_quantized_matmul(affon_rocm_session* session, const affon_rocm_qm
 /* The same operation without any device allocation. No counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). The
- * split-K partial sums that affon_rocm_quantized_matmul keeps in the
- * session's growable workspace go instead to a static 32 MiB device array
- * (one per GPU, held until the process ends), whose address is looked up
- * once per device when a session is created. Same selection, kernels and
- * results as affon_rocm_quantized_matmul; a shape whose split-K plan needs
- * more than 32 MiB of partial sums is rejected with AFFON_ROCM_UNSUPPORTED
- * before anything is enqueued (the output is untouched). Every call on a GPU
+ * scratch that affon_rocm_quantized_matmul keeps in the session's growable
+ * workspace (split-K partial sums; the reassociated prefill GEMM's per-group
+ * activation sums) goes instead to a static 33 MiB device array (one per
+ * GPU, held until the process ends), whose address is looked up on the first
+ * call on each device. Same selection, kernels and results as
+ * affon_rocm_quantized_matmul; a shape whose plan needs more than 33 MiB of
+ * scratch is rejected with AFFON_ROCM_UNSUPPORTED before anything is
+ * enqueued (the output is untouched). Every call on a GPU
  * shares that GPU's array, so calls that overlap on one GPU (other streams,
  * other sessions, other threads) race. */
 int affon_rocm_quantized_matmul_noalloc(affon_rocm_session* session, const affon_rocm_qmm_desc* desc);
@@ -167,6 +168,15 @@ typedef struct {
 int affon_rocm_read_floor_geometry(affon_rocm_session* session, const void* buffer, uint64_t bytes, void* sink,
                                    uint64_t sink_bytes, const affon_rocm_floor_geometry* geometry);
 int affon_rocm_empty_launch(affon_rocm_session* session, uint32_t blocks, uint32_t threads);
+
+/* Capability detail, no counterpart in the reference: validates like
+ * affon_rocm_quantized_matmul, then writes to *supported whether the guard of
+ * one physical kernel behind the candidates accepts the problem (1) or not
+ * (0). Kernel names: "generic", "gemv" (the gemv candidate), "gemv1" (its
+ * M = 1 kernel), "gemv_mfma", "mfma", "gemm_re" (the reassociated prefill
+ * GEMM), "gemm_pair" (the 4-bit prefill GEMM); another name is
+ * AFFON_ROCM_INVALID_SHAPE. Enqueues nothing. */
+int affon_rocm_kernel_supports(const affon_rocm_qmm_desc* desc, const char* kernel, int* supported);
 
 /* Runs validation and selection only and writes the selected implementation
  * id (e.g. "rocm_quantized_matmul.gemv") into id (capacity cap, NUL-terminated).

@@ -186,3 +186,39 @@ def test_rms_norm_rejects_non_positive_epsilon():
         with pytest.raises(TypeError, match="invalid rms_norm options"):
             program("norm", lambda p, eps=eps: rms_norm(p.argument("x", TensorSpec.f32([2, 4])), 1, epsilon=eps))
     program("norm", lambda p: rms_norm(p.argument("x", TensorSpec.f32([2, 4])), 1, epsilon=1e-6))
+
+
+def kernel_supports(d, kernel):
+    ok = ctypes.c_int(-1)
+    status = _native.load().affon_rocm_kernel_supports(ctypes.byref(d), kernel.encode(), ctypes.byref(ok))
+    assert status == 0, _native.last_error()
+    return ok.value
+
+
+def test_kernel_supports_names_and_validation():
+    d = make_desc(M=512, K=4096, N=256)
+    assert kernel_supports(d, "gemm_re") == 1
+    assert kernel_supports(d, "generic") == 1
+    ok = ctypes.c_int(-1)
+    assert _native.load().affon_rocm_kernel_supports(ctypes.byref(d), b"nope", ctypes.byref(ok)) == _native.INVALID_SHAPE
+    bad = make_desc(M=2, K=64, N=8)
+    bad.bits = 3
+    assert _native.load().affon_rocm_kernel_supports(ctypes.byref(bad), b"gemv", ctypes.byref(ok)) == _native.INVALID_SHAPE
+
+
+def test_reassociated_gemm_declines_offsets_past_31_bits():
+    """The reassociated prefill GEMM feeds its transfers 32-bit byte offsets
+    from a scalar base: the last activation row and the last packed-word row
+    must start below 2^31 bytes. Strided views (no memory is touched on the
+    CPU) put them just below and just at the bound."""
+    K, N, M = 4096, 256, 512
+    limit = 2**31
+    for xs0, accepted in ((limit // (2 * M) - 8, 1), (limit // (2 * M), 0)):
+        d = make_desc(M=M, K=K, N=N)
+        d.input = _view(4096, (M, K), (xs0, 1), _native.BF16)
+        assert kernel_supports(d, "gemm_re") == accepted, xs0
+    words = K // 8
+    for ws0, accepted in ((limit // (4 * N) - 4, 1), (limit // (4 * N), 0)):
+        d = make_desc(M=M, K=K, N=N)
+        d.packed = _view(4096, (N, words), (ws0, 1), _native.U32)
+        assert kernel_supports(d, "gemm_re") == accepted, ws0

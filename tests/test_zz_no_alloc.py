@@ -45,6 +45,9 @@ def test_noalloc_matches_allocating_entry_point():
         cases = [
             # prefill whose four K ranges fill the whole array: 4 x 512 x 4096 f32 = 32 MiB
             ((512, 4096, 14336), "approximate", "rocm_quantized_matmul.mfma"),
+            # the same shape under the default policy: the reassociated GEMM's four K ranges of partial
+            # sums (32 MiB) plus its per-group activation sums (768 KiB)
+            ((512, 4096, 14336), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma"),
             # a smaller decode batch with split K, reusing what the first call left in the array
             ((16, 4096, 4096), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma"),
         ]
