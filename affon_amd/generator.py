@@ -17,10 +17,28 @@ _EPSILON = 2.220446049250313e-16
 _CHUNK = 1 << 22
 
 
+_MAX_SAFE_INTEGER = 2**53 - 1
+
+
+def js_seed(seed) -> int:
+    """The generator state a seed starts from: `(Number.isSafeInteger(seed) ?
+    seed : 0) >>> 0` (program.ts:1386). Integral values within +-(2^53 - 1)
+    (ints, or floats with no fraction) keep their low 32 bits; anything else
+    (fractions, larger magnitudes, non-numbers) starts from 0."""
+    if isinstance(seed, bool) or not isinstance(seed, (int, float, np.integer, np.floating)):
+        return 0
+    if isinstance(seed, (float, np.floating)):
+        if not np.isfinite(seed) or seed != np.floor(seed):
+            return 0
+        seed = int(seed)
+    seed = int(seed)
+    return seed & 0xFFFFFFFF if abs(seed) <= _MAX_SAFE_INTEGER else 0
+
+
 def uniforms(seed: int, start: int, count: int) -> np.ndarray:
     """Uniforms number start .. start+count-1 of the mulberry32 stream."""
     i = np.arange(start + 1, start + count + 1, dtype=np.uint64)
-    t = (np.uint64(seed & 0xFFFFFFFF) + i * _GOLDEN) & _MASK
+    t = (np.uint64(js_seed(seed)) + i * _GOLDEN) & _MASK
     t = ((t ^ (t >> np.uint64(15))) * (t | np.uint64(1))) & _MASK
     t = t ^ ((t + (((t ^ (t >> np.uint64(7))) * (t | np.uint64(61))) & _MASK)) & _MASK)
     return ((t ^ (t >> np.uint64(14))) & _MASK).astype(np.float64) / 4294967296.0

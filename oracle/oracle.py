@@ -10,6 +10,7 @@ packed weights as uint32, all C-contiguous row-major.
 from __future__ import annotations
 
 import ctypes
+import math
 import pathlib
 
 import numpy as np
@@ -73,16 +74,26 @@ def f32_from_bf16(bits: np.ndarray) -> np.ndarray:
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def seed_state(seed) -> int:
+    """program.ts:1386: `(Number.isSafeInteger(seed) ? seed : 0) >>> 0`."""
+    if isinstance(seed, bool) or not isinstance(seed, (int, float)):
+        return 0
+    if isinstance(seed, float) and not (math.isfinite(seed) and seed == math.floor(seed)):
+        return 0
+    seed = int(seed)
+    return seed % 2**32 if -(2**53 - 1) <= seed <= 2**53 - 1 else 0
+
+
 def randn(seed: int, count: int, mean: float = 0.0, std: float = 1.0) -> tuple[np.ndarray, np.ndarray]:
     """Affon's Tensor.randn stream: (f32 values, their RNE bf16 bit patterns)."""
     f32 = np.empty(count, dtype=np.float32)
     bf16 = np.empty(count, dtype=np.uint16)
-    load().oracle_randn(seed, mean, std, count, f32.ctypes.data, bf16.ctypes.data)
+    load().oracle_randn(seed_state(seed), mean, std, count, f32.ctypes.data, bf16.ctypes.data)
     return f32, bf16
 
 
 def uniforms(seed: int, count: int) -> np.ndarray:
-    state = c_uint32(seed)
+    state = c_uint32(seed_state(seed))
     fn = load().oracle_mulberry32_next
     return np.array([fn(ctypes.byref(state)) for _ in range(count)], dtype=np.float64)
 

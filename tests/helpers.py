@@ -32,6 +32,25 @@ def unpack_bytes_le(packed: np.ndarray, bits: int) -> np.ndarray:
     return np.stack(parts, axis=-1).reshape(packed.shape[0], -1).astype(np.int64)
 
 
+def tie_group(bits: int, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """One quantization group of f32 values whose (w - b) / s is exactly k + 1/2
+    for the scale s = 2^-3 and bias b = -1.5 that quantizing it stores (both
+    exact in bf16, as is every value here): the group's minimum b, its
+    maximum b + (2^bits - 1) s, then a tie for each k = 0, 1, ... (at most
+    128 of them), the rest b. Returns (values, codes under round half to
+    even: k for even k, k + 1 for odd k). Rounding half away from zero gives
+    k + 1 for every tie, so it differs on every even k."""
+    levels = (1 << bits) - 1
+    s, b = 0.125, -1.5
+    values = np.full(group, b, np.float32)
+    codes = np.zeros(group, np.int64)
+    values[1], codes[1] = b + levels * s, levels
+    for k in range(max(0, min(levels, group - 2, 128))):
+        values[2 + k] = b + (k + 0.5) * s
+        codes[2 + k] = k if k % 2 == 0 else k + 1
+    return values, codes
+
+
 def storage(values, dtype: str) -> np.ndarray:
     """Host storage array for an operand given as f64 values: f32, or bf16 bits."""
     f32 = np.asarray(values, dtype=np.float64).astype(np.float32)

@@ -17,7 +17,7 @@ import affon_amd as A
 from affon_amd import _native
 from oracle import oracle as O
 from tests.helpers import (assert_bf16_product_close, assert_close_rtol_atol, fixture_operands, oracle_columns,
-                           pack_codes, peak_tolerance, reference_f64, storage)
+                           pack_codes, peak_tolerance, reference_f64, storage, tie_group, unpack_bytes_le)
 from tests.test_oracle import crossing_word_case, tile_edge_case
 
 pytestmark = pytest.mark.gpu
@@ -576,7 +576,11 @@ def test_quantize_bit_exact(session, bits, group, w_dtype, p_dtype):
     if w_dtype == "f32":
         w[4, :group] = -0.0        # signed zeros
         w[4, 1:group:2] = 0.0
+    # exact ties k + 1/2 for the stored scale and bias: rounding half to even is observable
+    ties, tie_codes = tie_group(bits, group)
+    w[5, group:2 * group] = O.bf16_from_f32(ties) if w_dtype == "bf16" else ties
     expected = O.quantize(w, bits, group, p_dtype)
+    np.testing.assert_array_equal(unpack_bytes_le(expected[0], bits)[5, group:2 * group], tie_codes)
     packed, scales, biases = A.quantize(upload(session, w, w_dtype), bits=bits, group_size=group,
                                         param_dtype=p_dtype)
     np.testing.assert_array_equal(packed.storage(), expected[0])

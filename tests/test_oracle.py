@@ -5,12 +5,15 @@ order, dropped bias, group index off by one, transposed operand, wrong
 rounding) fails at least one of them.
 """
 import math
+import pathlib
+import json
 
 import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import (fixture_operands, pack_codes, reference_f64, storage, unpack_bytes_le, widened)
+from tests.helpers import (fixture_operands, pack_codes, reference_f64, storage, tie_group, unpack_bytes_le,
+                           widened)
 
 
 def _operands(case):
@@ -240,6 +243,36 @@ def test_mulberry32_stream():
         assert O.uniforms(seed, 64).tolist() == _mulberry32_js(seed, 64)
 
 
+def _generator_vectors():
+    path = pathlib.Path(__file__).resolve().parent / "golden" / "generator_vectors.json"
+    return json.loads(path.read_text())["cases"]
+
+
+def _seed_value(text):
+    return float(text) if "." in text else int(text)
+
+
+def test_generator_matches_reference_js():
+    """The reference's own seededRandom and normal() (program.ts:1385-1413),
+    run under node by tests/golden/make_generator_vectors.py: uniforms exactly,
+    and Tensor.randn's f32 values (mean + std * normal(), rounded to f32) for
+    std 1 and 0.02, from the oracle's C generator and from the product's
+    vectorized one. The seeds include JS's seed normalization cases: negative,
+    past 2^32, not a safe integer (2^53), and fractional."""
+    from affon_amd import generator as G
+    for case in _generator_vectors():
+        seed = _seed_value(case["seed"])
+        uniforms = np.array([float(v) for v in case["uniforms"]])
+        np.testing.assert_array_equal(O.uniforms(seed, 64), uniforms, err_msg=f"oracle uniforms, seed {seed}")
+        np.testing.assert_array_equal(G.uniforms(seed, 0, 64), uniforms, err_msg=f"product uniforms, seed {seed}")
+        for key, std in (("f32_std1", 1.0), ("f32_std002", 0.02)):
+            want = np.array([float(v) for v in case[key]], dtype=np.float32)
+            got, _ = O.randn(seed, 65, mean=0.0, std=std)
+            np.testing.assert_array_equal(got, want, err_msg=f"oracle randn, seed {seed}, std {std}")
+            np.testing.assert_array_equal(G.normal_f32(seed, 65, 0.0, std), want,
+                                          err_msg=f"product randn, seed {seed}, std {std}")
+
+
 def test_randn_box_muller_and_moments():
     u = _mulberry32_js(7, 4)
     radius = math.sqrt(-2 * math.log(max(u[0], 2.220446049250313e-16)))
@@ -253,6 +286,32 @@ def test_randn_box_muller_and_moments():
 
 
 # ---- quantize / dequantize -----------------------------------------------------------------
+
+@pytest.mark.parametrize("bits,group", [(2, 8), (2, 32), (4, 3), (4, 32), (4, 64), (8, 16), (8, 256)])
+@pytest.mark.parametrize("param_dtype", ["f32", "bf16"])
+def test_quantize_rounds_exact_ties_to_even(bits, group, param_dtype):
+    """Groups whose (w - b) / s is exactly k + 1/2 for the stored scale and
+    bias (tests.helpers.tie_group): the codes are the even neighbours
+    (rintf, round half to even), which rounding half away from zero would
+    miss on every even k. The tie group sits in several group slots of a row
+    among random groups, with the rows' other groups untouched."""
+    per_word = 32 // bits
+    cols = int(np.lcm(per_word, group)) * 4
+    values, codes = tie_group(bits, group)
+    w, _ = O.randn(5, 3 * cols, 0.0, 0.02)
+    w = w.reshape(3, cols)
+    slots = [0, cols // group - 1]
+    for slot in slots:
+        w[1, slot * group:(slot + 1) * group] = values
+    packed, scales, biases = O.quantize(w, bits, group, param_dtype)
+    q = unpack_bytes_le(packed, bits)
+    for slot in slots:
+        np.testing.assert_array_equal(q[1, slot * group:(slot + 1) * group], codes, err_msg=f"group slot {slot}")
+        assert widened(scales[1:2, slot:slot + 1])[0, 0] == 0.125 and widened(biases[1:2, slot:slot + 1])[0, 0] == -1.5
+    ties = codes[2:2 + max(0, min((1 << bits) - 1, group - 2, 128))]
+    assert (ties != np.arange(1, ties.size + 1)).any(), "half-away rounding would give these codes"
+
+
 
 @pytest.mark.parametrize("bits,group", [(2, 32), (4, 64), (8, 64), (4, 32), (4, 128), (8, 16), (2, 8), (4, 48)])
 @pytest.mark.parametrize("param_dtype", ["f32", "bf16"])
