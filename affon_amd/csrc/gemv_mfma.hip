@@ -421,8 +421,9 @@ int vrow_layout(const QmmProblem& p) {
   return 0;
 }
 
-bool gemv_mfma_supports(const QmmProblem& p) {
-  if (vrow_layout(p) != 0) return true;
+namespace {
+// Whether the LDS-tiled kernel takes the problem.
+bool tiled_supports(const QmmProblem& p) {
   if (p.x_dtype != AFFON_ROCM_BF16 || p.M > (int64_t(1) << 20)) return false;
   if (p.xs1 != 1 || p.ws1 != 1 || p.ss1 != 1 || p.bs1 != 1) return false;
   // Each K step inside one group, groups addressed by shift.
@@ -436,6 +437,14 @@ bool gemv_mfma_supports(const QmmProblem& p) {
   if ((p.ss0 * pbytes) % 4 != 0 || (p.bs0 * pbytes) % 4 != 0 || (p.K / p.group * pbytes) % 4 != 0) return false;
   if (p.N > (int64_t(1) << 30) || p.K > (int64_t(1) << 30)) return false;
   return true;
+}
+}  // namespace
+
+bool gemv_mfma_supports(const QmmProblem& p) {
+  if (vrow_layout(p) != 0 || tiled_supports(p)) return true;
+  // Batches past the virtual-row kernels whose groups the tiled kernels do
+  // not take (groups of 32): the exact-plane GEMM.
+  return p.M > 4 && exact_supports(p);
 }
 
 namespace {
@@ -463,6 +472,7 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
     hipError_t e = hipSuccess;
     if (re_gemm_launch(p, l, &e, false)) return e;
   }
+  if (!tiled_supports(p)) return exact_launch(p, l);
   return tiled_launch(p, nullptr, 0, l);
 }
 

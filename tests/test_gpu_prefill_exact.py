@@ -1,0 +1,155 @@
+"""The exact-plane reassociated prefill GEMM (gemm_exact.hip): what the
+default policy runs for tall bf16 activations with 4-bit weights, bf16 scales
+and biases and groups of 32 (implementation rocm_quantized_matmul.gemv_mfma).
+
+Checks against f64 products computed here:
+  * exact -- integer activations in {-1, 0, 1}, codes below 16, scales with
+    full 8-bit bf16 significands (m / 64, m in [128, 255], so s*q needs up to
+    12 significant bits and both bf16 planes carry data) and integer biases:
+    every partial sum is a multiple of 2^-6 below 2^17, exact in f32, so the
+    output must equal the f64 product bit for bit. Shapes cover partial row
+    and column tiles, one and several K ranges, and K ranges whose group
+    count is not a multiple of 16 (a partial bias-term chunk);
+  * reassociated accuracy -- seeded random inputs, per element
+    |y - y64| <= 2^-18 * sum_k |x_k * w_k| with w = s*q + b in f64; the
+    approximate GEMM on the same inputs violates the bound;
+  * the fused output-bias and SiLU-gate epilogues, repeat determinism, and
+    the 2048 x 28672 x 8192 stress shape on sampled columns including the last
+    column tile, against f64.
+"""
+import numpy as np
+import pytest
+
+import affon_amd as A
+from oracle import oracle as O
+from tests.helpers import pack_codes, storage, widened
+from tests.test_gpu_parity import dtype_of, seeded_problem, upload
+from tests.test_gpu_prefill_reassociated import accuracy_ratio, product_f64
+
+pytestmark = pytest.mark.gpu
+
+GEMV_MFMA = "rocm_quantized_matmul.gemv_mfma"
+
+
+def exact_plane_operands(rng, M, N, K, group=32):
+    q = rng.integers(0, 16, size=(N, K))
+    x = rng.integers(-1, 2, size=(M, K)).astype(np.float64)
+    s = rng.integers(128, 256, size=(N, K // group)) / 64.0 * rng.choice([-1.0, 1.0], size=(N, K // group))
+    b = rng.integers(-2, 3, size=(N, K // group)).astype(np.float64)
+    return x, q, s, b
+
+
+def run_default(session, x, q, s, b, group=32):
+    xt = upload(session, storage(x, "bf16"), "bf16")
+    wt = upload(session, pack_codes(q, 4), "u32")
+    st, bt = upload(session, storage(s, "bf16"), "bf16"), upload(session, storage(b, "bf16"), "bf16")
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=group) == GEMV_MFMA
+    return A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=group).numpy()
+
+
+# (M, N, K): one row tile and 16 column tiles (several K ranges); partial row
+# and column tiles (several K ranges); 5 row tiles (the last partial) x 2
+# column tiles over one range of 24 groups (a partial bias-term chunk); short
+# batches past the virtual-row kernels (M = 5, 64) with a partial column tile.
+EXACT_SHAPES = [(256, 2048, 2048), (300, 200, 4096), (1100, 256, 768), (5, 384, 2048), (64, 130, 2048)]
+
+
+@pytest.mark.parametrize("shape", EXACT_SHAPES, ids=lambda s: "m{}_n{}_k{}".format(*s))
+def test_exact_plane_prefill_exact(session, shape, rng):
+    M, N, K = shape
+    x, q, s, b = exact_plane_operands(rng, M, N, K)
+    out = run_default(session, x, q, s, b)
+    cols = np.unique(np.concatenate([np.arange(min(N, 160)), np.linspace(0, N - 1, 96).astype(int)]))
+    np.testing.assert_array_equal(out[:, cols], product_f64(x, q, s, b, 32, cols).astype(np.float32),
+                                  err_msg=f"{shape}")
+
+
+def test_exact_plane_split_products_are_exact(session, rng):
+    """One nonzero activation per row picks single products x * s * q: each
+    output equals s*q (+ b, for the picked k's group) exactly, which fails if
+    either bf16 plane of s*q is dropped or rounded."""
+    M, N, K = 256, 256, 1024
+    _, q, s, b = exact_plane_operands(rng, M, N, K)
+    b[:] = 0.0
+    x = np.zeros((M, K))
+    picks = rng.integers(0, K, size=M)
+    x[np.arange(M), picks] = 1.0
+    out = run_default(session, x, q, s, b)
+    expected = (q[:, picks] * s[:, picks // 32]).T.astype(np.float32)
+    np.testing.assert_array_equal(out, expected)
+    # the products need more than bf16's 8 significant bits (both planes used)
+    assert (widened(storage(expected, "bf16")) != expected).any()
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 4096), (300, 640, 8192)])
+def test_exact_plane_prefill_accuracy(session, M, N, K):
+    x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=37)
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=32) == GEMV_MFMA
+    cols = np.unique(np.linspace(0, N - 1, 256).astype(int))
+    out = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=32).numpy()
+    bound = 2.0 ** -18
+    ratio = accuracy_ratio(out, x, packed, s, b, 32, cols)
+    assert ratio <= bound, f"reassociated: worst error {ratio:.3g} of sum|x*w| (bound {bound:.3g})"
+    approx = session.empty("f32", (M, N))
+    A.quantized_matmul_into(approx, xt, wt, st, bt, bits=4, group_size=32, implementation="mfma",
+                            policy="approximate")
+    assert accuracy_ratio(approx.numpy(), x, packed, s, b, 32, cols) > bound, "the bound does not separate the classes"
+
+
+def test_exact_plane_prefill_deterministic(session):
+    """Repeated runs (one and several K ranges) are bit-identical."""
+    for M, N, K in ((512, 2048, 2048), (512, 256, 8192)):
+        x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=41)
+        xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+        first = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=32).numpy()
+        for _ in range(2):
+            np.testing.assert_array_equal(A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=32).numpy(), first)
+
+
+def test_exact_plane_prefill_epilogues(session, rng):
+    """Output bias (f32, bf16) and the SiLU-gated product stored by the kernel
+    (one K range): bias bit-exact against plain + the same f32 add, the gate
+    within 6 ulp of silu(g) * u in f64."""
+    M, N, K = 256, 8192, 1024
+    x, gp, gs, gb = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=43)
+    _, upk, us, ub = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=47)
+    xt = upload(session, x, "bf16")
+    gate = tuple(upload(session, a, dtype_of(a)) for a in (gp, gs, gb))
+    up = tuple(upload(session, a, dtype_of(a)) for a in (upk, us, ub))
+    g = A.quantized_matmul(xt, *gate, bits=4, group_size=32).numpy()
+    u = A.quantized_matmul(xt, *up, bits=4, group_size=32).numpy()
+    for bias_dtype in ("f32", "bf16"):
+        bias_values = rng.standard_normal(N).astype(np.float32)
+        bias = storage(bias_values, "bf16") if bias_dtype == "bf16" else bias_values
+        fused = A.quantized_linear(xt, *gate, upload(session, bias, bias_dtype), bits=4, group_size=32).numpy()
+        np.testing.assert_array_equal(fused, (g + widened(bias).astype(np.float32)).astype(np.float32),
+                                      err_msg=bias_dtype)
+    fused = A.quantized_silu_gate(xt, gate, up, bits=4, group_size=32).numpy()
+    g64 = g.astype(np.float64)
+    with np.errstate(over="ignore"):
+        expected = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
+    bound = 6 * np.spacing(np.abs(expected).astype(np.float32)).astype(np.float64) + 1e-30
+    err = np.abs(fused.astype(np.float64) - expected)
+    assert np.all(err <= bound), f"worst {float(err.max())}"
+
+
+def test_exact_plane_prefill_stress_full_size(session):
+    """The 2048 x 28672 x 8192 stress configuration under the default policy:
+    W f32 [28672, 8192] N(0, 0.02) quantized on the GPU at 4 bits, group 32,
+    bf16 parameters; x bf16 [2048, 8192] N(0, 1). Every row of 112 sampled
+    columns (the first and last column tiles among them) against f64 within
+    the reassociated bound."""
+    M, N, K = 2048, 28672, 8192
+    wf, _ = O.randn(2, N * K, 0.0, 0.02)
+    _, xb = O.randn(1, M * K, 0.0, 1.0)
+    x = xb.reshape(M, K)
+    packed, scales, biases = A.quantize(upload(session, wf.reshape(N, K), "f32"), bits=4, group_size=32,
+                                        param_dtype="bf16")
+    del wf
+    xt = upload(session, x, "bf16")
+    assert A.selected_implementation(xt, packed, scales, biases, bits=4, group_size=32) == GEMV_MFMA
+    out = A.quantized_matmul(xt, packed, scales, biases, bits=4, group_size=32).numpy()
+    cols = np.unique(np.concatenate([np.arange(16), np.linspace(0, N - 1, 80).astype(int), np.arange(N - 16, N)]))
+    ratio = accuracy_ratio(out, x, packed.storage(), scales.storage(), biases.storage(), 32, cols)
+    assert ratio <= 2.0 ** -18, f"worst error {ratio:.3g} of sum|x*w|"
