@@ -413,14 +413,6 @@ hipError_t launch_typed(const TileArgs& args, hipStream_t stream) {
 
 // Which virtual-row layout runs a problem: 1 = 8 rows per wave, 2 = 16 rows
 // per wave, 0 = neither (the LDS-tiled kernel below).
-int vrow_layout(const QmmProblem& p) {
-  vrow::Plan eight;
-  vrow16::Plan sixteen;
-  if (vrow::plan(p, &eight)) return 1;
-  if (vrow16::plan(p, &sixteen)) return 2;
-  return 0;
-}
-
 namespace {
 // Whether the LDS-tiled kernel takes the problem.
 bool tiled_supports(const QmmProblem& p) {
@@ -440,6 +432,22 @@ bool tiled_supports(const QmmProblem& p) {
 }
 }  // namespace
 
+int vrow_layout(const QmmProblem& p) {
+  // The LDS-tiled kernel takes the batch whenever it can from two activation
+  // rows on for 8-bit codes and from three rows on for 2- and 4-bit codes:
+  // measured on 14336 x 4096 weights (graph periods, one box) it is as fast
+  // or faster there than either virtual-row layout (8-bit M = 2: 14.0 against
+  // 15.2 us, M = 4: 14.0 against 17.0 us; 4-bit M = 4: 10.9 against 11.6 us),
+  // while at two rows 2- and 4-bit codes run 1 % faster on the 16-row layout.
+  if (p.M >= (p.bits == 8 ? 2 : 3) && tiled_supports(p)) return 0;
+  vrow::Plan eight;
+  vrow16::Plan sixteen;
+  if (vrow::plan(p, &eight)) return 1;
+  if (vrow16::plan(p, &sixteen)) return 2;
+  return 0;
+}
+
+
 bool gemv_mfma_supports(const QmmProblem& p) {
   if (vrow_layout(p) != 0 || tiled_supports(p)) return true;
   // Batches past the virtual-row kernels whose groups the tiled kernels do
@@ -452,8 +460,8 @@ hipError_t tiled_launch(const QmmProblem& p, const QmmProblem* group, int count,
 }  // namespace
 
 hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
-  // M <= 4: a virtual-row kernel (packed words straight into the B operand,
-  // no LDS for weights); larger batches: the LDS-tiled kernel.
+  // A virtual-row kernel (packed words straight into the B operand, no LDS
+  // for weights) where vrow_layout picks one; otherwise the LDS-tiled kernel.
   switch (vrow_layout(p)) {
     case 1:
       return vrow_launch_b8(p, l.stream);
@@ -557,7 +565,7 @@ bool gemv_mfma_group_supports(const QmmProblem* group, int count) {
   const QmmProblem& p = group[0];
   for (int i = 0; i < count; ++i) {
     const QmmProblem& q = group[i];
-    if (!gemv_mfma_supports(q) || vrow_layout(q) != 0) return false;  // the LDS-tiled kernel only
+    if (!tiled_supports(q) || vrow_layout(q) != 0) return false;  // the LDS-tiled kernel only
     if (q.epi.kind != kEpiNone && q.epi.kind != kEpiBias) return false;
     if (q.x != p.x || q.xs0 != p.xs0 || q.M != p.M || q.K != p.K || q.bits != p.bits || q.group != p.group ||
         q.p_dtype != p.p_dtype || q.ws0 != p.ws0 || q.ss0 != p.ss0 || q.bs0 != p.bs0)

@@ -224,9 +224,10 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, gro
     """Projections of one input in one launch (M = 1: the gemv kernel; M = 8
     and 16 with bf16 activations: the LDS-tiled gemv_mfma kernel, at 8 rows
     with twin column tiles, whose split-K partials span all projections) or
-    in sequence (M = 2), with output biases
-    on some of them; ragged sizes exercise the padding between projections.
-    Group 32 at 4 and 8 bits takes the M=1 kernel's per-lane parameter loads."""
+    in sequence (M = 2 on the virtual-row kernels; groups of 32 past M = 4 on
+    the exact-plane GEMM), with output biases on some of them; ragged sizes
+    exercise the padding between projections. Group 32 at 4 and 8 bits takes
+    the M=1 kernel's per-lane parameter loads."""
     K = 1024
     for M in (1, 2, 8, 16):
         projections, host = [], []
@@ -242,7 +243,9 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, gro
             host.append((packed, s, b, bias))
         xt = upload(session, x, dtype_of(x))
         plan = A.grouped_plan(xt, projections, bits=bits, group_size=group)
-        one_launch = M == 1 or (M in (8, 16) and x_dtype == "bf16" and group % 64 == 0)  # tiled: K steps of 64
+        # The tiled kernel (K steps of 64) takes M = 8, 16 and, for 8-bit codes, M = 2.
+        tiled_m = (2, 8, 16) if bits == 8 else (8, 16)
+        one_launch = M == 1 or (M in tiled_m and x_dtype == "bf16" and group % 64 == 0)
         if one_launch:
             kernel = "gemv" if M == 1 else "gemv_mfma"
             assert plan == f"rocm_quantized_matmul.{kernel}[grouped:{len(sizes)},bias]", plan

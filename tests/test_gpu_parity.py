@@ -437,24 +437,25 @@ def test_gemv_mfma_exact_integer_products(session, bits, p_dtype, rng):
         np.testing.assert_array_equal(out.numpy(), expected.astype(np.float32), err_msg=f"{M}x{N}x{K} g{group}")
 
 
-VROW_CASES = {  # (M, N, K, group)
+VROW_CASES = {  # (M, N, K, group); groups of 32 and 16 keep M = 3, 4 on the virtual-row kernels
     8: [(1, 77, 1024, 64), (2, 300, 512, 32), (2, 129, 2048, 16), (4, 1000, 2048, 64), (8, 64, 4096, 64),
-        (6, 200, 1024, 64)],
+        (6, 200, 1024, 64), (3, 200, 1024, 32), (4, 90, 2048, 16)],
     4: [(1, 77, 4096, 64), (2, 300, 1024, 128), (1, 129, 1024, 32), (4, 1000, 2048, 64), (8, 40, 8192, 128),
-        (5, 50, 4096, 128)],
-    2: [(1, 77, 2048, 64), (2, 300, 2048, 128), (4, 129, 4096, 128), (3, 50, 2048, 128)],
+        (5, 50, 4096, 128), (4, 300, 1024, 32), (3, 129, 2048, 32)],
+    2: [(1, 77, 2048, 64), (2, 300, 2048, 128), (4, 129, 4096, 128), (3, 50, 2048, 128), (2, 129, 4096, 64)],
 }
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("p_dtype", ["bf16", "f32"])
 def test_virtual_row_decode_exact_integer_products(session, bits, p_dtype, rng):
-    """Small-M decode on the matrix cores (M <= 2 at 8 bits: the 8-row
-    virtual-row layout; M <= 4: the 16-row layout; larger M: the LDS-tiled
-    kernel): integer codes and activations with power-of-two scales and
-    integer biases make every partial sum exact, so the output must equal the
-    f64 reference exactly. Partial row blocks, 1-4 groups per MFMA span, and
-    1, 2 or 4 K-parts per row."""
+    """Small-M decode on the matrix cores (the 8-row virtual-row layout at 8
+    bits and M <= 2, the 16-row layout up to M = 4, the LDS-tiled kernel for
+    larger M and wherever it is the faster one: from M = 2 at 8 bits and
+    M = 3 otherwise, for the groups it takes): integer codes and activations
+    with power-of-two scales and integer biases make every partial sum exact,
+    so the output must equal the f64 reference exactly. Partial row blocks,
+    1-4 groups per MFMA span, and 1, 2 or 4 K-parts per row."""
     for M, N, K, group in VROW_CASES[bits]:
         q = rng.integers(0, 1 << bits, size=(N, K))
         x = rng.integers(-3, 4, size=(M, K)).astype(np.float64)

@@ -79,6 +79,22 @@ def test_grouped_selection_from_specs():
     batch = [member(32, 4096), member(32, 1024), member(32, 1024)]  # the LDS-tiled kernel does
     assert grouped_select_for_specs(batch, opts, "backend_equivalent") == "rocm_quantized_matmul.gemv_mfma[grouped:3]"
 
+    def member_g32(m, n):
+        return [TensorSpec.bf16([m, 4096]), TensorSpec.u32([n, 512]), TensorSpec.bf16([n, 128]),
+                TensorSpec.bf16([n, 128])]
+    # Groups of 32 past M = 4 run on the exact-plane GEMM, which takes no groups.
+    batch = [member_g32(8, 4096), member_g32(8, 1024)]
+    assert grouped_select_for_specs(batch, {"bits": 4, "group_size": 32}, "backend_equivalent") == \
+        "rocm_quantized_matmul.gemv_mfma;rocm_quantized_matmul.gemv_mfma"
+
+    def member_b8(m, n):
+        return [TensorSpec.bf16([m, 4096]), TensorSpec.u32([n, 1024]), TensorSpec.bf16([n, 64]),
+                TensorSpec.bf16([n, 64])]
+    # At 8 bits the tiled kernel takes M = 2.
+    batch = [member_b8(2, 4096), member_b8(2, 1024)]
+    assert grouped_select_for_specs(batch, {"bits": 8, "group_size": 64}, "backend_equivalent") == \
+        "rocm_quantized_matmul.gemv_mfma[grouped:2]"
+
 
 @pytest.mark.parametrize("case", ["silu_alone", "shared_gate", "gate_is_output", "bias_matrix", "different_inputs",
                                   "mul_plain", "add_two_projections"])
