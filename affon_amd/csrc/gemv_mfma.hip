@@ -133,7 +133,7 @@ template <int BITS, typename PT, int XROWS, bool PWHOLE, int WS = (BITS == 8 ? (
 __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   TileArgs a = args;
   constexpr int kXLoads = XROWS / 8;  // activation DMA instructions per step
-  using P = Plan<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst>;
+  using P = Plan<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst, 16>;
   constexpr int RB = RowBlocks<XROWS>::kBlocks;
   constexpr int kRows = RowBlocks<XROWS>::kRows;
   constexpr bool kTwin = XROWS == 8;             // twin column tiles
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     for (int i = 0; i < kXLoads; ++i)
       load_lds<16>(x_src[i] + (s0 + step) * kBK, lds_address(lds_x[wave][step & 3]) + 1024 * i);
   };
-  WeightStream<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst> ws;
+  WeightStream<BITS, PT, kXLoads, PWHOLE, WS, kActsFirst, 16> ws;
   // PWHOLE keeps one window per wave: both window buffers of the wave, which
   // are adjacent when indexed [wave][buffer].
   uint8_t* p_base = PWHOLE ? lds_p[0][0] + wave * 2 * P::kPBytes : lds_p[0][wave];
@@ -329,8 +329,11 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
   // wave's own activation ring (no transfer into it is in flight any more):
   // output element i of row block rb and column tile ct is row 16rb + 4h + i,
   // column 16ct + r; with twin tiles, accumulator ca holds row 4(h%2) + i of
-  // column tile 2ca + h/2. Added in wave order.
+  // column tile 2ca + h/2. Added in wave order. Column col of row row sits at
+  // col ^ (16 * (row/4 % 2)): the two lane quarters of a 32-lane LDS phase
+  // write rows four apart, which then land on different banks.
   auto ysum = [&](int w) { return reinterpret_cast<float*>(&lds_x[w][0][0]); };
+  auto ypos = [](int row, int col) { return row * kCols + (col ^ (16 * ((row >> 2) & 1))); };
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -339,7 +342,7 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
       for (int i = 0; i < 4; ++i) {
         const int row = kTwin ? 4 * (h & 1) + i : 16 * rb + 4 * h + i;
         const int ct = kTwin ? 2 * ca + (h >> 1) : ca;
-        ysum(wave)[row * kCols + 16 * ct + r] = y[rb][ca][i];
+        ysum(wave)[ypos(row, 16 * ct + r)] = y[rb][ca][i];
       }
   __syncthreads();
   float* dst = a.partial + split * static_cast<int64_t>(a.M) * pstride;
@@ -351,7 +354,8 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
         const int o = e * kThreads + tid;
         const int row = m0 + o / kCols, col = n0 + o % kCols;
         if (row < a.M && col < a.N) {
-          const float v = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
+          const int q = ypos(o / kCols, o % kCols);
+          const float v = ((ysum(0)[q] + ysum(1)[q]) + ysum(2)[q]) + ysum(3)[q];
           store_as<KIND>(a.epi, a.out + static_cast<int64_t>(row) * a.N + col, col, v);
         }
       }
@@ -361,8 +365,9 @@ __global__ __launch_bounds__(kThreads, 1) void qskinny_kernel(TileArgs args) {
     for (int e = 0; e < kOutRows * kCols / kThreads; ++e) {
       const int o = e * kThreads + tid;
       const int row = m0 + o / kCols, col = n0 + o % kCols;
+      const int q = ypos(o / kCols, o % kCols);
       if (row < a.M && col < a.N)
-        dst[static_cast<int64_t>(row) * pstride + col_base + col] = ((ysum(0)[o] + ysum(1)[o]) + ysum(2)[o]) + ysum(3)[o];
+        dst[static_cast<int64_t>(row) * pstride + col_base + col] = ((ysum(0)[q] + ysum(1)[q]) + ysum(2)[q]) + ysum(3)[q];
     }
   }
 }
