@@ -9,18 +9,19 @@ Affon's seeded generator (x: seed 1 N(0,1); W: seed 2 N(0,0.02), quantized on
 the GPU). `roofline_prefill` is the M=512 prefill of the same weight format
 (x bf16 [512, 4096], W [14336, 4096]) as its configuration describes it
 (decoded weights rounded to bf16 and fed to bf16 MFMA: the approximate
-policy) against the bf16 MFMA peak; the default policy's unrounded GEMM is
-timed beside it. The same run
-measures, as extra fields, the 8-bit decode sweep M in {1,2,4,8,16}, 4-bit
-M=16, both prefill orientations (approximate and default policies), the
-2048-row group-32 stress shapes, the Llama-8B-shaped layer sequences at M=1
-and M=32, and the f32 4096x4096 4-bit case.
+policy) against the bf16 MFMA peak, with the reference's CPU kernel timed on
+a sample of its output columns beside it; the default policy's unrounded
+GEMM is timed beside it. The same run measures, as extra fields, the 8-bit
+decode sweep M in {1,2,4,8,16}, 4-bit M=16, both prefill orientations
+(approximate and default policies), the 2048-row group-32 stress shapes
+(approximate and default policies), the Llama-8B-shaped layer sequences at
+M=1 and M=32, and the f32 4096x4096 4-bit case.
 
 Timing: the K timed steps are captured once into a HIP graph on the session's
-stream; after an untimed replay, the graph is replayed REPLAYS times, each
-bracketed by HIP events recorded on that stream, and the median replay gives
-the per-step time: the GPU's back-to-back launch period without host
-overhead. Weight sets are rotated (>= 9 sets, > 600 MB in total) so that the
+stream; after about 0.1 s of untimed replays (the clock settles under the
+load), the graph is replayed REPLAYS times, each bracketed by HIP events
+recorded on that stream, and the median replay gives the per-step time: the
+GPU's back-to-back launch period without host overhead. Weight sets are rotated (>= 9 sets, > 600 MB in total) so that the
 256 MB Infinity Cache cannot hold the working set.
 
 Prints one JSON line. --gpus N with N > 1 exits: this path runs on one GPU.
@@ -82,6 +83,28 @@ def algorithmic_bytes(M, N, K, bits, group, xbytes, pbytes):
     return N * K * bits // 8 + 2 * N * (K // group) * pbytes + M * K * xbytes + M * N * 4
 
 
+SETTLE_S = 0.1
+
+
+def settle(hip: Hip, session, replay) -> None:
+    """Untimed replays until about SETTLE_S seconds of GPU time have passed,
+    so that the timed replays run at the clock the GPU settles to under this
+    load (matrix-core work lowers it within tens of milliseconds)."""
+    stream = ctypes.c_void_p(session.stream)
+    start, stop = hip.event(), hip.event()
+    hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
+    replay()
+    hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
+    hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+    ms = ctypes.c_float()
+    hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+    for _ in range(min(1000, int(SETTLE_S * 1e3 / max(ms.value, 1e-3)))):
+        replay()
+    session.synchronize()
+    hip.lib.hipEventDestroy(start)
+    hip.lib.hipEventDestroy(stop)
+
+
 class Workload:
     def __init__(self, session, name, M, N, K, bits, group, x_dtype="bf16", p_dtype="bf16", policy="backend_equivalent",
                  w_dtype=None, seed_x=1, seed_w=2):
@@ -138,8 +161,7 @@ class Workload:
                 self.launch(i)
             hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
             hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-            hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")  # untimed replay
-            self.session.synchronize()
+            settle(hip, self.session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
         start, stop = hip.event(), hip.event()
         runs = []
         for _ in range(REPLAYS):
@@ -190,8 +212,7 @@ class Workload:
             launch(i)
         hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
         hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-        hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-        self.session.synchronize()
+        settle(hip, self.session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
         start, stop = hip.event(), hip.event()
         runs = []
         for _ in range(REPLAYS):
@@ -232,7 +253,8 @@ def _host_cores() -> int:
     return max(1, min(16, cores))  # the GPU box's CPU share is 16 cores
 
 
-def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, threads: int = 1) -> dict:
+def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, threads: int = 1,
+                 unit: str = "GB/s") -> dict:
     """The reference's scalar CPU kernel as restated in oracle/cpu_baseline.c
     (one specialised loop per bit width and dtype pair, ordered f32, decode
     inside the dot product), timed on this host over a bounded sample of
@@ -269,12 +291,14 @@ def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, thr
     xbytes = 2 if work.x_dtype == "bf16" else 4
     pbytes = 2 if work.p_dtype == "bf16" else 4
     sample_bytes = passes * algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
+    sample_flops = passes * 2 * M * rows * K
     check = min(rows, 512)
     ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, check))
     if not np.array_equal(out[:, :check].view(np.uint32), ref[:, :check].view(np.uint32)):
         raise AssertionError("CPU baseline loop differs from the oracle")
     err = float(np.abs(gpu_out[:, :rows].astype(np.float64) - out[:, :rows]).max())
-    return {"value": round(sample_bytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+    value = sample_bytes / elapsed / 1e9 if unit == "GB/s" else sample_flops / elapsed / 1e12
+    return {"value": round(value, 6), "unit": unit, "cores": threads, "kind": "port",
             "sample": (f"reference CPU kernel restated (oracle/cpu_baseline.c: scalar, specialised per bits and "
                        f"dtype pair, ordered f32) over the timed workload, "
                        + (f"{passes} whole passes" if rows == N else f"rows 0..{rows} of {N} ({rows / N:.1%})")
@@ -423,8 +447,7 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
         launch_all(i)
     hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
     hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-    hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-    session.synchronize()
+    settle(hip, session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
     start, stop = hip.event(), hip.event()
     times = []
     for _ in range(REPLAYS):
@@ -451,7 +474,8 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
 def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
     """Per-launch milliseconds of `steps` launches captured in one HIP graph
     on the session stream, for each of REPLAYS replays (after `warmup`
-    direct launches and one untimed replay). launch(i) enqueues launch i."""
+    direct launches and about 0.1 s of untimed replays). launch(i) enqueues
+    launch i."""
     stream = ctypes.c_void_p(session.stream)
     for i in range(warmup):
         launch(i)
@@ -462,8 +486,7 @@ def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
         launch(i)
     hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
     hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-    hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-    session.synchronize()
+    settle(hip, session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
     start, stop = hip.event(), hip.event()
     runs = []
     for _ in range(REPLAYS):
@@ -652,7 +675,7 @@ def main() -> int:
                  f"{extras['cpu_baseline_all_cores']['value']} GB/s on {extras['cpu_baseline_all_cores']['cores']}")
     main_work.release()
 
-    def record(name, work, bound="hbm"):
+    def record(name, work, bound="hbm", keep=False):
         t = work.time(hip, args.steps, args.warmup, use_graph)
         entry = {"implementation": work.implementation, "us_per_step": round(t * 1e3, 3),
                  "us_per_step_replays": [round(v * 1e3, 3) for v in work.replay_ms],
@@ -664,7 +687,8 @@ def main() -> int:
             entry["mfma_frac"] = round(entry["TFLOP/s"] / BF16_MFMA_PEAK_TFLOPS, 4)
         extras[name] = entry
         progress(f"{name}: {entry['us_per_step']} us per step ({work.implementation})")
-        work.release()
+        if not keep:
+            work.release()
         return t
 
     for M in (1, 2, 4, 8, 16):
@@ -675,11 +699,17 @@ def main() -> int:
                        ("prefill_4bit_g64_m512_n4096_k14336", 4096, 14336)):
         if want(name):
             work = Workload(session, name, 512, N, K, 4, 64, policy="approximate")
-            t = record(name, work, bound="mfma")
+            t = record(name, work, bound="mfma", keep=True)
             extras[name]["numerical_policy"] = "approximate"
             if roofline_prefill is None:
                 roofline_prefill = roofline_gemm(work, t, load_traffic(name))
                 roofline_prefill["kernel_us_replays"] = extras[name]["us_per_step_replays"]
+                if args.cpu_seconds > 0:
+                    # The reference's CPU kernel on a sample of output columns (every activation row).
+                    roofline_prefill["cpu_baseline"] = cpu_baseline(work, work.out.numpy(), args.cpu_seconds,
+                                                                    unit="TFLOP/s")
+                    progress(f"prefill CPU baseline: {roofline_prefill['cpu_baseline']['value']} TFLOP/s on 1 thread")
+            work.release()
     # The same prefills under the default policy (backend_equivalent: no rounding of decoded weights).
     for name, N, K in (("prefill_4bit_g64_m512_n14336_k4096_backend_equivalent", 14336, 4096),
                        ("prefill_4bit_g64_m512_n4096_k14336_backend_equivalent", 4096, 14336)):
@@ -692,6 +722,12 @@ def main() -> int:
         if want(name):
             record(name, Workload(session, name, 2048, N, K, 4, 32, policy="approximate"), bound="mfma")
             extras[name]["numerical_policy"] = "approximate"
+    # The same stress shapes under the default policy (the exact-plane GEMM).
+    for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192_backend_equivalent", 28672, 8192),
+                       ("prefill_4bit_g32_m2048_n8192_k28672_backend_equivalent", 8192, 28672)):
+        if want(name):
+            record(name, Workload(session, name, 2048, N, K, 4, 32), bound="mfma")
+            extras[name]["numerical_policy"] = "backend_equivalent"
     if want("decode_4bit_g64_m16"):
         record("decode_4bit_g64_m16", Workload(session, "decode_4bit_g64_m16", 16, 14336, 4096, 4, 64))
     for M in (1, 32):
