@@ -19,9 +19,11 @@ M=1 and M=32, and the f32 4096x4096 4-bit case.
 
 Timing: the K timed steps are captured once into a HIP graph on the session's
 stream; after about 0.1 s of untimed replays (the clock settles under the
-load), the graph is replayed REPLAYS times, each bracketed by HIP events
-recorded on that stream, and the median replay gives the per-step time: the
-GPU's back-to-back launch period without host overhead. Weight sets are rotated (>= 9 sets, > 600 MB in total) so that the
+load), one untimed replay and then REPLAYS timed replays are enqueued back to
+back, with a HIP event on that stream between consecutive replays. The median
+interval over K gives the per-step time: the GPU's back-to-back launch
+period, without host overhead (the graph's launch latency falls in the
+untimed replay). Weight sets are rotated (>= 9 sets, > 600 MB in total) so that the
 256 MB Infinity Cache cannot hold the working set.
 
 Prints one JSON line. --gpus N with N > 1 exits: this path runs on one GPU.
@@ -149,41 +151,29 @@ class Workload:
         """Milliseconds per step: the median over REPLAYS timed runs of `steps`
         back-to-back launches (graph replays, or direct launches with
         --launch stream). Every run's figure is kept in self.replay_ms."""
+        if use_graph:
+            self.replay_ms = time_graph(hip, self.session, self.launch, steps, warmup)
+            return median(self.replay_ms)
         stream = ctypes.c_void_p(self.session.stream)
         for i in range(warmup):
             self.launch(i)
         self.session.synchronize()
-        exe = graph = None
-        if use_graph:
-            graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
-            hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed
-            for i in range(steps):
-                self.launch(i)
-            hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
-            hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-            settle(hip, self.session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
         start, stop = hip.event(), hip.event()
         runs = []
         for _ in range(REPLAYS):
             hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-            if use_graph:
-                hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-            else:
-                for i in range(steps):
-                    self.launch(i)
+            for i in range(steps):
+                self.launch(i)
             hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
             hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
             ms = ctypes.c_float()
             hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
             runs.append(ms.value / steps)
         self.session.synchronize()
-        if use_graph:
-            hip.lib.hipGraphExecDestroy(exe)
-            hip.lib.hipGraphDestroy(graph)
         hip.lib.hipEventDestroy(start)
         hip.lib.hipEventDestroy(stop)
         self.replay_ms = runs
-        return sorted(runs)[len(runs) // 2]
+        return median(runs)
 
     def time_read_floor(self, hip: Hip, steps: int, warmup: int) -> float:
         """Milliseconds per launch of affon_rocm_read_floor over the same
@@ -202,32 +192,7 @@ class Workload:
                 from affon_amd import _native
                 raise RuntimeError(_native.last_error())
 
-        stream = ctypes.c_void_p(self.session.stream)
-        for i in range(warmup):
-            launch(i)
-        self.session.synchronize()
-        graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
-        hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
-        for i in range(steps):
-            launch(i)
-        hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
-        hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-        settle(hip, self.session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
-        start, stop = hip.event(), hip.event()
-        runs = []
-        for _ in range(REPLAYS):
-            hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-            hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-            hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
-            hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
-            ms = ctypes.c_float()
-            hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
-            runs.append(ms.value / steps)
-        hip.lib.hipGraphExecDestroy(exe)
-        hip.lib.hipGraphDestroy(graph)
-        hip.lib.hipEventDestroy(start)
-        hip.lib.hipEventDestroy(stop)
-        return sorted(runs)[len(runs) // 2]
+        return median(time_graph(hip, self.session, launch, steps, warmup))
 
     def host_operands(self):
         packed, scales, biases = self.weights[0]
@@ -437,31 +402,7 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
                 from affon_amd import _native
                 raise RuntimeError(_native.last_error())
 
-    stream = ctypes.c_void_p(session.stream)
-    for i in range(warmup):
-        launch_all(i)
-    session.synchronize()
-    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
-    hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
-    for i in range(steps):
-        launch_all(i)
-    hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
-    hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-    settle(hip, session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
-    start, stop = hip.event(), hip.event()
-    times = []
-    for _ in range(REPLAYS):
-        hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-        hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-        hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
-        hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
-        ms = ctypes.c_float()
-        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
-        times.append(ms.value / steps)
-    hip.lib.hipGraphExecDestroy(exe)
-    hip.lib.hipGraphDestroy(graph)
-    hip.lib.hipEventDestroy(start)
-    hip.lib.hipEventDestroy(stop)
+    times = time_graph(hip, session, launch_all, steps, warmup)
     t = sorted(times)[len(times) // 2]
     tensors.clear()
     built.clear()
@@ -475,32 +416,38 @@ def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
     """Per-launch milliseconds of `steps` launches captured in one HIP graph
     on the session stream, for each of REPLAYS replays (after `warmup`
     direct launches and about 0.1 s of untimed replays). launch(i) enqueues
-    launch i."""
+    launch i. All replays are enqueued back to back behind one untimed lead-in
+    replay, with an event between consecutive replays: each timed interval is
+    one replay's launches, and the graph's launch latency falls in the
+    lead-in."""
     stream = ctypes.c_void_p(session.stream)
     for i in range(warmup):
         launch(i)
     session.synchronize()
     graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
-    hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+    hip.check(hip.lib.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed
     for i in range(steps):
         launch(i)
     hip.check(hip.lib.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
     hip.check(hip.lib.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
-    settle(hip, session, lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch"))
-    start, stop = hip.event(), hip.event()
+    replay = lambda: hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+    settle(hip, session, replay)
+    events = [hip.event() for _ in range(REPLAYS + 1)]
+    replay()  # lead-in
+    for e in range(REPLAYS + 1):
+        hip.check(hip.lib.hipEventRecord(events[e], stream), "hipEventRecord")
+        if e < REPLAYS:
+            replay()
+    hip.check(hip.lib.hipEventSynchronize(events[-1]), "hipEventSynchronize")
     runs = []
-    for _ in range(REPLAYS):
-        hip.check(hip.lib.hipEventRecord(start, stream), "hipEventRecord")
-        hip.check(hip.lib.hipGraphLaunch(exe, stream), "hipGraphLaunch")
-        hip.check(hip.lib.hipEventRecord(stop, stream), "hipEventRecord")
-        hip.check(hip.lib.hipEventSynchronize(stop), "hipEventSynchronize")
+    for e in range(REPLAYS):
         ms = ctypes.c_float()
-        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop), "hipEventElapsedTime")
+        hip.check(hip.lib.hipEventElapsedTime(ctypes.byref(ms), events[e], events[e + 1]), "hipEventElapsedTime")
         runs.append(ms.value / steps)
     hip.lib.hipGraphExecDestroy(exe)
     hip.lib.hipGraphDestroy(graph)
-    hip.lib.hipEventDestroy(start)
-    hip.lib.hipEventDestroy(stop)
+    for e in events:
+        hip.lib.hipEventDestroy(e)
     return runs
 
 
