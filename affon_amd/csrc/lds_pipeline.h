@@ -221,34 +221,36 @@ struct Plan {
 
   // LANE_COLS: the consumer's lanes read LANE_COLS consecutive columns per
   // instruction (16: the decode-batch kernel, lanes 16q + r on column
-  // 16t + r; 32: the 128-row GEMM, lanes 32h + r on column 32t + r). The
-  // swizzles use only the column bits below LANE_COLS, so that the columns
-  // one lane reads differ by a constant address offset (an instruction
-  // immediate, no per-read address arithmetic).
+  // 16t + r; 32: the 128-row GEMM, lanes 32h + r on column 32t + r).
   static_assert(LANE_COLS == 16 || LANE_COLS == 32, "lane layouts of the consumers");
   // Slot (16-byte unit) holding part `part` of column c's run (c_i = bit i
-  // of c). 128-byte runs: part XOR (c1 ^ c4, c2 ^ c5, c3) for 16 lane
-  // columns, part XOR (c1 ^ c4, c2, c3) for 32. 64-byte runs: part XOR (c2,
-  // c3), and part XOR (c1 ^ c4, c3). Under the bank model above the 4-bit
-  // (b64) and 8-bit (b128) reads of both consumers are conflict-free; 2-bit
-  // runs of 64 bytes keep a 2-way conflict that no XOR of column bits removes
-  // (16 columns x 2 lanes per phase over 8 bank positions). The c4, c5 terms
-  // (constant within one read) give the four column tiles of the 16-column
-  // layout different slot orders: reads whose addresses differ by a multiple
-  // of 512 bytes would otherwise be merged into one ds_read2st64, whose two
-  // halves share banks.
+  // of c).
+  //
+  // 16 lane columns (the decode-batch kernel): 128-byte runs part XOR
+  // (c1 ^ c4, c2 ^ c5, c3), 64-byte runs part XOR (c2, c3). Under the bank
+  // model above its 4-bit (b64) and 8-bit (b128) reads are conflict-free, and
+  // the counters agree; 2-bit runs of 64 bytes keep a 2-way conflict that no
+  // XOR of column bits removes (16 columns x 2 lanes per phase over 8 bank
+  // positions). The c4, c5 terms (constant within one read) give the four
+  // column tiles different slot orders: reads whose addresses differ by a
+  // multiple of 512 bytes would otherwise be merged into one ds_read2st64,
+  // whose two halves share banks.
+  //
+  // 32 lane columns (the 128-row GEMM): part XOR (c0..c2) XOR c3 for
+  // 128-byte runs and part XOR ((c1 ^ c3), (c2 ^ c4)) for 64-byte runs. Its
+  // counters show 0.30 of LDS-active cycles in conflicts with these, and
+  // 0.01 with the decode kernel's kind of layout, which made the GEMM 0.5 to
+  // 1.6 % slower (more address arithmetic): these stay.
   static __device__ __forceinline__ int slot(int c, int part) {
     if constexpr (LANE_COLS == 16)
       return kSlots == 8 ? part ^ ((c >> 1) & 7) ^ ((c >> 4) & 3) : part ^ ((c >> 2) & 3);
-    const int flip = ((c >> 1) ^ (c >> 4)) & 1;
-    return kSlots == 8 ? part ^ flip ^ (((c >> 2) & 3) << 1) : part ^ flip ^ (((c >> 3) & 1) << 1);
+    return kSlots == 8 ? part ^ (c & 7) ^ ((c >> 3) & 1) : part ^ (((c >> 1) ^ (c >> 3)) & 3);
   }
   // Dword holding logical dword d of column c's 16-byte parameter window, and
-  // of its 32-byte whole-range window (PWHOLE): the LANE_COLS columns of one
-  // read land on distinct banks.
-  static __device__ __forceinline__ int p_dword(int c, int d) {
-    return d ^ ((c >> 3) & (LANE_COLS == 16 ? 1 : 3));
-  }
+  // of its 32-byte whole-range window (PWHOLE): for the decode kernel the 16
+  // columns of one read land on distinct banks; the GEMM's windows are not
+  // swizzled (as for its slots).
+  static __device__ __forceinline__ int p_dword(int c, int d) { return LANE_COLS == 16 ? d ^ ((c >> 3) & 1) : d; }
   static __device__ __forceinline__ int p_whole_dword(int c, int d) { return d ^ ((c >> 2) & 3); }
 
   // Whether iteration j issues a packed-word transfer, and how many steps
@@ -378,9 +380,11 @@ struct WeightStream {
     n_cols = a.N;
     // Instruction i carries columns whose swizzle term depends only on i % 2
     // and lane / 32 (columns 8i + L/8: bits 2, 3 are bit 0 of i and lane bit 5).
+    if constexpr (PWHOLE) {
 #pragma unroll
-    for (int odd = 0; odd < 2; ++odd)
-      p_whole_off[odd] = 4 * min(window(s0) + P::p_whole_dword(8 * odd + (lane >> 3), lane & 7), row_dwords - 1);
+      for (int odd = 0; odd < 2; ++odd)
+        p_whole_off[odd] = 4 * min(window(s0) + P::p_whole_dword(8 * odd + (lane >> 3), lane & 7), row_dwords - 1);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int col = min(n0 + 16 * i + (lane >> 2), a.N - 1);
@@ -445,7 +449,7 @@ struct WeightStream {
     const int g = (((s0 + step) * kBK + k) >> (5 + group_shift)) - window(s0 + (step & ~3)) * (4 / PT::bytes);
     const uint8_t* pbuf = p_lds(step);
     if constexpr (PT::bytes == 2) {
-      const int byte = 16 * c + 4 * P::p_dword(c, g >> 1) + 2 * (g & 1);
+      const int byte = LANE_COLS == 16 ? 16 * c + 4 * P::p_dword(c, g >> 1) + 2 * (g & 1) : 16 * c + 2 * g;
       *s_raw = *reinterpret_cast<const uint16_t*>(pbuf + byte);
       *b_raw = *reinterpret_cast<const uint16_t*>(pbuf + 1024 + byte);
     } else {
