@@ -412,6 +412,35 @@ def layer_sequence(session, hip: Hip, M: int, steps: int, warmup: int, fused: bo
             "TFLOP/s": round(flops / (t * 1e-3) / 1e12, 3), "algorithmic_bytes": nbytes, "weight_sets": sets}
 
 
+def quantize_stress(session, hip: Hip, steps: int, warmup: int) -> dict:
+    """Quantize of the 2048-row stress shape's first weight matrix: f32 W
+    [28672, 8192] (seed 2, N(0, 0.02)) to 4-bit codes with bf16 scales and
+    biases in groups of 32, through affon_rocm_quantize into preallocated
+    outputs. Algorithmic bytes: the f32 read, the packed codes and both
+    parameter planes (1,086,324,736). W (940 MB) exceeds the 256 MB MALL, so
+    every launch reads it from HBM."""
+    from affon_amd import _native
+    N, K, bits, group = 28672, 8192, 4, 32
+    w = session.randn((N, K), seed=2, std=0.02, dtype="f32")
+    packed = session.empty("u32", (N, K * bits // 32))
+    scales = session.empty("bf16", (N, K // group))
+    biases = session.empty("bf16", (N, K // group))
+    lib = _native.load()
+
+    def launch(i):
+        _native.check(lib.affon_rocm_quantize(session._handle, w.data_ptr, _native.F32, N, K, bits, group,
+                                              packed.data_ptr, scales.data_ptr, biases.data_ptr, _native.BF16),
+                      "quantize")
+
+    times = time_graph(hip, session, launch, steps, warmup)
+    t = median(times)
+    nbytes = N * K * 4 + N * K * bits // 8 + 2 * N * (K // group) * 2
+    return {"us_per_step": round(t * 1e3, 3), "us_per_step_replays": [round(v * 1e3, 3) for v in times],
+            "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": nbytes, "shape": [N, K], "bits": bits, "group_size": group,
+            "weight_dtype": "f32", "param_dtype": "bf16"}
+
+
 def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
     """Per-launch milliseconds of `steps` launches captured in one HIP graph
     on the session stream, for each of REPLAYS replays (after `warmup`
@@ -686,6 +715,9 @@ def main() -> int:
     if want("decode_4bit_g64_f32_4096"):
         record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
                                                     x_dtype="f32", p_dtype="f32"))
+    if want("quantize_4bit_g32_28672x8192"):
+        extras["quantize_4bit_g32_28672x8192"] = quantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
+        progress(f"quantize_4bit_g32_28672x8192: {extras['quantize_4bit_g32_28672x8192']['us_per_step']} us per step")
 
     result = {
         "metric": METRIC,

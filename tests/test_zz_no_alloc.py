@@ -13,6 +13,7 @@ import pytest
 
 import affon_amd as A
 from affon_amd import _native, ops
+from tests.helpers import HipRuntime
 
 pytestmark = pytest.mark.gpu
 
@@ -68,3 +69,54 @@ def test_noalloc_matches_allocating_entry_point():
         # The allocating entry point runs it.
         status, out, message = run(session, "affon_rocm_quantized_matmul", operands, "approximate")
         assert status == 0 and np.isfinite(out).all(), message
+
+
+def test_noalloc_under_graph_capture():
+    """The use the entry point is for: calls captured into a HIP graph on the
+    session stream and replayed. Both captured plans keep scratch in the
+    static array (the default-policy prefill: split-K partial sums and
+    per-group activation sums; a decode batch with split K). Between replays
+    the program runs eager no-allocation calls of other shapes, which leave
+    other contents in the array, and clears the outputs; every replay must
+    reproduce the eager results bit for bit."""
+    hip = HipRuntime()
+    lib = _native.load()
+    with A.Session("rocm") as session:
+        shapes = [((512, 4096, 14336), "backend_equivalent"), ((16, 4096, 4096), "backend_equivalent")]
+        # Each descriptor holds raw device pointers: its operand tensors stay
+        # referenced here for as long as the descriptor (and the graph) is used.
+        calls = []
+        for (M, N, K), policy in shapes:
+            operands = problem(session, M, N, K, seed=M + 7)
+            out = session.tensor(np.full((M, N), 7.0, np.float32))
+            desc = ops._descriptor(*operands, 4, 64, out, "auto", policy)
+            calls.append((desc, out, operands))
+        eager = []
+        for desc, out, _ in calls:  # eager first: the first call on the device looks the array up
+            assert lib.affon_rocm_quantized_matmul_noalloc(session._handle, ctypes.byref(desc)) == 0, \
+                _native.last_error()
+            session.synchronize()
+            eager.append(out.numpy().copy())
+
+        def enqueue():
+            for desc, _, _ in calls:
+                status = lib.affon_rocm_quantized_matmul_noalloc(session._handle, ctypes.byref(desc))
+                assert status == 0, _native.last_error()
+
+        graph = hip.capture(session.stream, enqueue)
+        try:
+            other = problem(session, 64, 2048, 8192, seed=11)
+            for i in range(3):
+                status, _, message = run(session, "affon_rocm_quantized_matmul_noalloc", other, "backend_equivalent")
+                assert status == 0, message
+                for _, out, _ in calls:
+                    zeros = np.zeros(out.shape, np.float32)
+                    _native.check(lib.affon_rocm_memcpy_h2d(session._handle, out.data_ptr, zeros.ctypes.data,
+                                                            zeros.nbytes), "clear")
+                session.synchronize()
+                hip.replay(session.stream, graph)
+                for (_, out, _), want in zip(calls, eager):
+                    np.testing.assert_array_equal(out.numpy().view(np.uint32), want.view(np.uint32),
+                                                  err_msg=f"replay {i}, output {out.shape}")
+        finally:
+            hip.destroy(graph)
