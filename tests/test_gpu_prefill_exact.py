@@ -14,8 +14,8 @@ Checks against f64 products computed here:
     |y - y64| <= 2^-18 * sum_k |x_k * w_k| with w = s*q + b in f64; the
     approximate GEMM on the same inputs violates the bound;
   * the fused output-bias and SiLU-gate epilogues, repeat determinism, and
-    the 2048 x 28672 x 8192 stress shape on sampled columns including the last
-    column tile, against f64.
+    both orientations of the 2048-row stress shape on sampled columns
+    including the first and last column tiles, against f64.
 """
 import numpy as np
 import pytest
@@ -135,21 +135,25 @@ def test_exact_plane_prefill_epilogues(session, rng):
 
 
 def test_exact_plane_prefill_stress_full_size(session):
-    """The 2048 x 28672 x 8192 stress configuration under the default policy:
-    W f32 [28672, 8192] N(0, 0.02) quantized on the GPU at 4 bits, group 32,
-    bf16 parameters; x bf16 [2048, 8192] N(0, 1). Every row of 112 sampled
-    columns (the first and last column tiles among them) against f64 within
-    the reassociated bound."""
-    M, N, K = 2048, 28672, 8192
-    wf, _ = O.randn(2, N * K, 0.0, 0.02)
-    _, xb = O.randn(1, M * K, 0.0, 1.0)
-    x = xb.reshape(M, K)
-    packed, scales, biases = A.quantize(upload(session, wf.reshape(N, K), "f32"), bits=4, group_size=32,
-                                        param_dtype="bf16")
-    del wf
-    xt = upload(session, x, "bf16")
-    assert A.selected_implementation(xt, packed, scales, biases, bits=4, group_size=32) == GEMV_MFMA
-    out = A.quantized_matmul(xt, packed, scales, biases, bits=4, group_size=32).numpy()
-    cols = np.unique(np.concatenate([np.arange(16), np.linspace(0, N - 1, 80).astype(int), np.arange(N - 16, N)]))
-    ratio = accuracy_ratio(out, x, packed.storage(), scales.storage(), biases.storage(), 32, cols)
-    assert ratio <= 2.0 ** -18, f"worst error {ratio:.3g} of sum|x*w|"
+    """The 2048-row stress configuration under the default policy, both
+    orientations: W f32 [28672, 8192] N(0, 0.02) (the same values reshaped to
+    [8192, 28672] for the second) quantized on the GPU at 4 bits, group 32,
+    bf16 parameters; x bf16 [2048, 8192] N(0, 1), its rows repeated to 28672
+    columns for the second orientation. Every row of 112 sampled columns (the
+    first and last column tiles among them) against f64 within the
+    reassociated bound."""
+    M = 2048
+    wf, _ = O.randn(2, 28672 * 8192, 0.0, 0.02)
+    _, xb = O.randn(1, M * 8192, 0.0, 1.0)
+    x8 = xb.reshape(M, 8192)
+    for N, K in ((28672, 8192), (8192, 28672)):
+        packed, scales, biases = A.quantize(upload(session, wf.reshape(N, K), "f32"), bits=4, group_size=32,
+                                            param_dtype="bf16")
+        x = x8 if K == 8192 else np.ascontiguousarray(np.tile(x8, (1, -(-K // 8192)))[:, :K])
+        xt = upload(session, x, "bf16")
+        assert A.selected_implementation(xt, packed, scales, biases, bits=4, group_size=32) == GEMV_MFMA
+        out = A.quantized_matmul(xt, packed, scales, biases, bits=4, group_size=32).numpy()
+        cols = np.unique(np.concatenate([np.arange(16), np.linspace(0, N - 1, 80).astype(int), np.arange(N - 16, N)]))
+        ratio = accuracy_ratio(out, xt.storage(), packed.storage(), scales.storage(), biases.storage(), 32, cols)
+        assert ratio <= 2.0 ** -18, f"{N}x{K}: worst error {ratio:.3g} of sum|x*w|"
+        del packed, scales, biases, xt, out
