@@ -538,7 +538,7 @@ int affon_rocm_kernel_supports(const affon_rocm_qmm_desc* desc, const char* kern
   } kGuards[] = {
       {"generic", affon::generic_supports}, {"gemv", affon::gemv_supports},     {"gemv1", affon::gemv1_supports},
       {"gemv_mfma", affon::gemv_mfma_supports}, {"mfma", affon::mfma_supports}, {"gemm_re", affon::re_gemm_supports},
-      {"gemm_pair", affon::pair_supports},  {"gemm_exact", affon::exact_supports},
+      {"gemm_pair", affon::pair_supports},  {"gemm_re32", affon::re32_supports},
   };
   for (const auto& g : kGuards) {
     if (std::strcmp(g.name, kernel) == 0) {

@@ -456,8 +456,8 @@ int vrow_layout(const QmmProblem& p) {
 bool gemv_mfma_supports(const QmmProblem& p) {
   if (vrow_layout(p) != 0 || tiled_supports(p)) return true;
   // Batches past the virtual-row kernels whose groups the tiled kernels do
-  // not take (groups of 32): the exact-plane GEMM.
-  return p.M > 4 && exact_supports(p);
+  // not take (groups of 32): the group-32 GEMM.
+  return p.M > 4 && re32_supports(p);
 }
 
 namespace {
@@ -485,7 +485,7 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
     hipError_t e = hipSuccess;
     if (re_gemm_launch(p, l, &e, false)) return e;
   }
-  if (!tiled_supports(p)) return exact_launch(p, l);
+  if (!tiled_supports(p)) return re32_launch(p, l);
   return tiled_launch(p, nullptr, 0, l);
 }
 

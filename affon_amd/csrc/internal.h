@@ -116,11 +116,11 @@ bool re_gemm_supports(const QmmProblem& p);
 // which mfma_launch runs.
 bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status, bool rounded);
 
-// The reassociated prefill GEMM with exact two-plane weights (gemm_exact.hip),
-// which gemv_mfma_launch runs for tall activations whose groups the
-// group-scaling GEMM and the LDS-tiled kernel do not take (groups of 32).
-bool exact_supports(const QmmProblem& p);
-hipError_t exact_launch(const QmmProblem& p, const Launch& l);
+// The reassociated prefill GEMM for groups of 32 (gemm_re32.hip), which
+// gemv_mfma_launch runs for tall activations whose groups the group-scaling
+// GEMM and the LDS-tiled kernel do not take.
+bool re32_supports(const QmmProblem& p);
+hipError_t re32_launch(const QmmProblem& p, const Launch& l);
 
 bool mfma_supports(const QmmProblem& p);
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l);

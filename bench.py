@@ -698,7 +698,7 @@ def main() -> int:
         if want(name):
             record(name, Workload(session, name, 2048, N, K, 4, 32, policy="approximate"), bound="mfma")
             extras[name]["numerical_policy"] = "approximate"
-    # The same stress shapes under the default policy (the exact-plane GEMM).
+    # The same stress shapes under the default policy (the group-32 reassociated GEMM).
     for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192_backend_equivalent", 28672, 8192),
                        ("prefill_4bit_g32_m2048_n8192_k28672_backend_equivalent", 8192, 28672)):
         if want(name):

@@ -174,8 +174,8 @@ int affon_rocm_empty_launch(affon_rocm_session* session, uint32_t blocks, uint32
  * one physical kernel behind the candidates accepts the problem (1) or not
  * (0). Kernel names: "generic", "gemv" (the gemv candidate), "gemv1" (its
  * M = 1 kernel), "gemv_mfma", "mfma", "gemm_re" (the group-scaling
- * reassociated prefill GEMM), "gemm_exact" (the exact-plane reassociated
- * prefill GEMM), "gemm_pair" (the 4-bit prefill GEMM); another name is
+ * reassociated prefill GEMM), "gemm_re32" (the reassociated prefill GEMM for
+ * groups of 32), "gemm_pair" (the 4-bit prefill GEMM); another name is
  * AFFON_ROCM_INVALID_SHAPE. Enqueues nothing. */
 int affon_rocm_kernel_supports(const affon_rocm_qmm_desc* desc, const char* kernel, int* supported);
 

@@ -225,7 +225,7 @@ def test_grouped_projections_against_oracle(session, x_dtype, p_dtype, bits, gro
     and 16 with bf16 activations: the LDS-tiled gemv_mfma kernel, at 8 rows
     with twin column tiles, whose split-K partials span all projections) or
     in sequence (M = 2 on the virtual-row kernels; groups of 32 past M = 4 on
-    the exact-plane GEMM), with output biases on some of them; ragged sizes
+    the group-32 GEMM), with output biases on some of them; ragged sizes
     exercise the padding between projections. Group 32 at 4 and 8 bits takes
     the M=1 kernel's per-lane parameter loads."""
     K = 1024

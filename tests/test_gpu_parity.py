@@ -612,7 +612,7 @@ def test_prefill_stress_full_size_sampled(session):
     sampled columns per orientation (the first and last 16, which lie in the
     first and last column tiles, and 80 spread over the rest) against the
     oracle, within the bf16-input tolerance. The default policy's run of the
-    same shapes: tests/test_gpu_prefill_exact.py."""
+    same shapes: tests/test_gpu_prefill_g32.py."""
     wf, _ = O.randn(2, 28672 * 8192, 0.0, 0.02)
     _, xb = O.randn(1, 2048 * 8192, 0.0, 1.0)
     x = xb.reshape(2048, 8192)

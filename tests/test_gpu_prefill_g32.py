@@ -1,15 +1,16 @@
-"""The exact-plane reassociated prefill GEMM (gemm_exact.hip): what the
+"""The reassociated prefill GEMM for groups of 32 (gemm_re32.hip): what the
 default policy runs for tall bf16 activations with 4-bit weights, bf16 scales
 and biases and groups of 32 (implementation rocm_quantized_matmul.gemv_mfma).
 
 Checks against f64 products computed here:
   * exact -- integer activations in {-1, 0, 1}, codes below 16, scales with
-    full 8-bit bf16 significands (m / 64, m in [128, 255], so s*q needs up to
-    12 significant bits and both bf16 planes carry data) and integer biases:
-    every partial sum is a multiple of 2^-6 below 2^17, exact in f32, so the
-    output must equal the f64 product bit for bit. Shapes cover partial row
-    and column tiles, one and several K ranges, and K ranges whose group
-    count is not a multiple of 16 (a partial bias-term chunk);
+    full 8-bit bf16 significands (m / 64, m in [128, 255], so s * sum(x*q)
+    needs up to 17 significant bits) and integer biases: every partial sum is
+    a multiple of 2^-6 below 2^17, exact in f32, so the output must equal the
+    f64 product bit for bit. Shapes cover partial row and column tiles, one
+    and several K ranges, bias-term rounds of 64 groups (one partial, several
+    with a partial last one) and K = 2 mod 4 steps (a last packed-word run of
+    two steps);
   * reassociated accuracy -- seeded random inputs, per element
     |y - y64| <= 2^-18 * sum_k |x_k * w_k| with w = s*q + b in f64; the
     approximate GEMM on the same inputs violates the bound;
@@ -31,7 +32,7 @@ pytestmark = pytest.mark.gpu
 GEMV_MFMA = "rocm_quantized_matmul.gemv_mfma"
 
 
-def exact_plane_operands(rng, M, N, K, group=32):
+def exact_operands(rng, M, N, K, group=32):
     q = rng.integers(0, 16, size=(N, K))
     x = rng.integers(-1, 2, size=(M, K)).astype(np.float64)
     s = rng.integers(128, 256, size=(N, K // group)) / 64.0 * rng.choice([-1.0, 1.0], size=(N, K // group))
@@ -47,29 +48,33 @@ def run_default(session, x, q, s, b, group=32):
     return A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=group).numpy()
 
 
-# (M, N, K): one row tile and 16 column tiles (several K ranges); partial row
-# and column tiles (several K ranges); 5 row tiles (the last partial) x 2
-# column tiles over one range of 24 groups (a partial bias-term chunk); short
-# batches past the virtual-row kernels (M = 5, 64) with a partial column tile.
-EXACT_SHAPES = [(256, 2048, 2048), (300, 200, 4096), (1100, 256, 768), (5, 384, 2048), (64, 130, 2048)]
+# (M, N, K): one row tile and 16 column tiles (four K ranges); partial row
+# and column tiles (eight K ranges); 5 row tiles (the last partial) x 2
+# column tiles over one range of 24 groups (a partial bias-term round); short
+# batches past the virtual-row kernels (M = 5, 64) with a partial column tile;
+# K = 1152 and 4224 (18 and 66 steps: one range whose last packed-word run
+# holds two steps; 36 and 132 groups: one and three bias-term rounds, the
+# last partial).
+EXACT_SHAPES = [(256, 2048, 2048), (300, 200, 4096), (1100, 256, 768), (5, 384, 2048), (64, 130, 2048),
+                (130, 200, 1152), (600, 300, 4224)]
 
 
 @pytest.mark.parametrize("shape", EXACT_SHAPES, ids=lambda s: "m{}_n{}_k{}".format(*s))
-def test_exact_plane_prefill_exact(session, shape, rng):
+def test_g32_prefill_exact(session, shape, rng):
     M, N, K = shape
-    x, q, s, b = exact_plane_operands(rng, M, N, K)
+    x, q, s, b = exact_operands(rng, M, N, K)
     out = run_default(session, x, q, s, b)
     cols = np.unique(np.concatenate([np.arange(min(N, 160)), np.linspace(0, N - 1, 96).astype(int)]))
     np.testing.assert_array_equal(out[:, cols], product_f64(x, q, s, b, 32, cols).astype(np.float32),
                                   err_msg=f"{shape}")
 
 
-def test_exact_plane_split_products_are_exact(session, rng):
+def test_g32_single_products_are_exact(session, rng):
     """One nonzero activation per row picks single products x * s * q: each
-    output equals s*q (+ b, for the picked k's group) exactly, which fails if
-    either bf16 plane of s*q is dropped or rounded."""
+    output equals s*q exactly (biases zero), which fails if the code or the
+    scale of the picked k's group is wrong or s*q is rounded to bf16."""
     M, N, K = 256, 256, 1024
-    _, q, s, b = exact_plane_operands(rng, M, N, K)
+    _, q, s, b = exact_operands(rng, M, N, K)
     b[:] = 0.0
     x = np.zeros((M, K))
     picks = rng.integers(0, K, size=M)
@@ -77,12 +82,12 @@ def test_exact_plane_split_products_are_exact(session, rng):
     out = run_default(session, x, q, s, b)
     expected = (q[:, picks] * s[:, picks // 32]).T.astype(np.float32)
     np.testing.assert_array_equal(out, expected)
-    # the products need more than bf16's 8 significant bits (both planes used)
+    # the products need more than bf16's 8 significant bits
     assert (widened(storage(expected, "bf16")) != expected).any()
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 1024, 4096), (300, 640, 8192)])
-def test_exact_plane_prefill_accuracy(session, M, N, K):
+def test_g32_prefill_accuracy(session, M, N, K):
     x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=37)
     xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
     assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=32) == GEMV_MFMA
@@ -97,7 +102,7 @@ def test_exact_plane_prefill_accuracy(session, M, N, K):
     assert accuracy_ratio(approx.numpy(), x, packed, s, b, 32, cols) > bound, "the bound does not separate the classes"
 
 
-def test_exact_plane_prefill_deterministic(session):
+def test_g32_prefill_deterministic(session):
     """Repeated runs (one and several K ranges) are bit-identical."""
     for M, N, K in ((512, 2048, 2048), (512, 256, 8192)):
         x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=41)
@@ -107,7 +112,7 @@ def test_exact_plane_prefill_deterministic(session):
             np.testing.assert_array_equal(A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=32).numpy(), first)
 
 
-def test_exact_plane_prefill_epilogues(session, rng):
+def test_g32_prefill_epilogues(session, rng):
     """Output bias (f32, bf16) and the SiLU-gated product stored by the kernel
     (one K range): bias bit-exact against plain + the same f32 add, the gate
     within 6 ulp of silu(g) * u in f64."""
@@ -134,7 +139,7 @@ def test_exact_plane_prefill_epilogues(session, rng):
     assert np.all(err <= bound), f"worst {float(err.max())}"
 
 
-def test_exact_plane_prefill_stress_full_size(session):
+def test_g32_prefill_stress_full_size(session):
     """The 2048-row stress configuration under the default policy, both
     orientations: W f32 [28672, 8192] N(0, 0.02) (the same values reshaped to
     [8192, 28672] for the second) quantized on the GPU at 4 bits, group 32,

@@ -82,7 +82,7 @@ def test_grouped_selection_from_specs():
     def member_g32(m, n):
         return [TensorSpec.bf16([m, 4096]), TensorSpec.u32([n, 512]), TensorSpec.bf16([n, 128]),
                 TensorSpec.bf16([n, 128])]
-    # Groups of 32 past M = 4 run on the exact-plane GEMM, which takes no groups.
+    # Groups of 32 past M = 4 run on the group-32 GEMM, which takes no groups.
     batch = [member_g32(8, 4096), member_g32(8, 1024)]
     assert grouped_select_for_specs(batch, {"bits": 4, "group_size": 32}, "backend_equivalent") == \
         "rocm_quantized_matmul.gemv_mfma;rocm_quantized_matmul.gemv_mfma"
