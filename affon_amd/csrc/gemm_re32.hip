@@ -60,16 +60,17 @@ constexpr int kPlaneRound = 64;                   // plane entries per row stage
 static_assert(kAOps == 4 && kWOps == 2 && kSOps == 1, "transfer counts assumed by the issue slots and waits");
 static_assert(3 * kRows * kPlaneRound * 2 <= kAStages * kAStage, "a round of the three planes fits the ring");
 
-// vmcnt bound at the start of iteration j (= step % 4). Iteration t issues
-// the activations of step t+2 and, when t % 4 == 0, the packed words and the
-// scale windows of steps t+4 .. t+7, in that order; the prologue issues the
-// words and windows of steps 0..3 and the activations of steps 0 and 1. At
-// the start of iteration t the activations of step t (issued by iteration
-// t-2) must have landed, and with them everything issued before: the words
-// and windows of the step and of the next one, which are read during t.
-// In flight may stay the words and windows issued by iteration t-2 (when
-// t-2 = 0 mod 4) and every transfer of iteration t-1.
-constexpr int wait_at(int j) { return kAOps + (j == 1 || j == 2 ? kWOps + kSOps : 0); }
+// vmcnt bound before the barrier of step t (j = t % 4), which sits between
+// the step's third and fourth phase. Before it, step t issues the
+// activations of step t+2 and, when t % 4 == 0, then the packed words and
+// scale windows of steps t+4 .. t+7; the prologue issues the words and
+// windows of steps 0..3, then the activations of steps 0 and 1. At the
+// barrier of step t the activations of step t+1 (issued by step t-1) must
+// have landed, for the fragment reads of step t+1 that follow it, and with
+// them everything issued before: the words and windows that the next steps
+// read at their start. In flight may stay the words and windows issued by
+// step t-1 (when t-1 = 0 mod 4) and every transfer of step t.
+constexpr int mid_wait(int j) { return kAOps + (j == 0 || j == 1 ? kWOps + kSOps : 0); }
 
 // Slot (16-byte unit) of part `part` (0..7) in local column c's 128-byte
 // packed run.
@@ -159,34 +160,33 @@ struct Re32Args {
   int groups;              // groups per parameter row (K / 32)
 };
 
-// MFMA of slot s (0..15) of a step: tiles 0, 1 then 2, 3 of the first group
-// (slots 0..7), then the same for the second (8..15); within four slots the
-// two tiles alternate, first chunk then second.
-constexpr int slot_tile(int s) { return 2 * ((s / 4) % 2) + s % 2; }
-constexpr int slot_kk(int s) { return 2 * (s / 8) + (s % 4) / 2; }
-// A tile's group is complete after slot L (an odd kk: L % 4 >= 2); its 16
-// multiply-adds y += s * sums run in slots L+3 (elements 0..5), L+4 (6..10)
-// and L+5 (11..15), before slot L+6 starts its next group from zero. Slots
-// past 15 are the next step's (for the second group of tiles 1, 2, 3).
-constexpr bool group_done(int l) { return l % 4 >= 2; }
-constexpr int part_first(int d) { return d == 3 ? 0 : d == 4 ? 6 : 11; }
-constexpr int part_end(int d) { return d == 3 ? 6 : d == 4 ? 11 : 16; }
-
 // Steps: a multiple of 4 per K range, or (a single range) 2 mod 4, whose
 // last run of packed words holds two steps.
-__global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
+//
+// Schedule. A step is four phases; an MFMA phase is one group's eight MFMAs
+// (kk = 2G, 2G+1 of tiles 0..3; the first of each tile starts from zero), a
+// vector phase the 64 multiply-adds y += s * sums of one group, the decode
+// of two of the next step's packed words, the LDS reads of the next MFMA
+// phase's fragments and the step's transfers. The two waves of a SIMD (mi =
+// 0, 1) run them in opposite order, so that one wave's MFMAs run while the
+// other wave's vector instructions issue:
+//   mi = 0:  MFMA group 1 | vector group 1 | MFMA group 2 | barrier | vector group 2
+//   mi = 1:  vector group 2 of the previous step | MFMA group 1 | vector group 1 | barrier | MFMA group 2
+// Every read of step t's activation stage comes before the barrier of step
+// t (mi = 0 reads its first-group fragments after the barrier of step t-1),
+// and the next write of that stage (the activations of step t+3) is issued
+// by step t+1, after it. The packed words and scales a step reads at its
+// start are ordered against their transfers by earlier barriers the same way.
+template <int MI>
+__device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uint8_t* lds_w, uint8_t* lds_s) {
   const TileArgs& a = r.t;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a[kAStages * kAStage];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_w[2 * kWBuf];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s[2 * kSBuf];
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int li = lane & 31;
   const int lh = lane >> 5;
-  const int mi = wave >> 2;  // rows 128*mi ..
-  const int ni = wave & 3;   // columns 32*ni ..
+  constexpr int mi = MI;    // rows 128*mi ..
+  const int ni = wave & 3;  // columns 32*ni ..
 
   const int nb_n = (a.N + kCols - 1) / kCols;
   int tile, split;
@@ -283,19 +283,8 @@ __global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
   for (int i = 0; i < kAOps; ++i) issue_a1(0, 0, i);
 #pragma unroll
   for (int i = 0; i < kAOps; ++i) issue_a1(min(1, last), 1, i);
-  wait_vmcnt<2 * kAOps>();  // the words and windows of steps 0..3
+  wait_vmcnt<kAOps>();  // the words and windows of steps 0..3, the activations of step 0
   __syncthreads();
-  bf16x8_t bq[4];  // B operands of the step, by kk
-  {
-    const u32x4_t w = read_w(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      CodeTmp d;
-      code_piece<0>(w[kk], d, bq[kk]);
-      code_piece<1>(w[kk], d, bq[kk]);
-      code_piece<2>(w[kk], d, bq[kk]);
-    }
-  }
 
   f32x16_t y[4], acc[4];
 #pragma unroll
@@ -303,10 +292,44 @@ __global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       y[T][v] = 0.0f;
-      acc[T][v] = 0.0f;  // the second group of "step -1" is scaled by 0 in the first step
+      acc[T][v] = 0.0f;  // mi = 1: the second group of "step -1" is scaled by 0 in the first step
     }
   const f32x16_t zero = {};
-  float sb_prev = 0.0f;  // second-group scale of the previous step
+  float sb_prev = 0.0f;  // mi = 1: second-group scale of the previous step
+  bf16x8_t bq[4];        // B operands of the step, by kk
+  bf16x8_t af[8];        // fragments of one MFMA phase: MFMA i is tile i % 4, kk 2G + i / 4
+  u32x4_t wprev = read_w(0, 0);  // mi = 1: the words whose second group the next first phase decodes
+  auto decode2 = [&](const u32x4_t& w, int kk0) {
+#pragma unroll
+    for (int k = kk0; k < kk0 + 2; ++k) {
+      CodeTmp d;
+      code_piece<0>(w[k], d, bq[k]);
+      code_piece<1>(w[k], d, bq[k]);
+      code_piece<2>(w[k], d, bq[k]);
+    }
+  };
+  auto read_group = [&](int stage, int G) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) af[i] = read_a(stage, i % 4, 2 * G + i / 4);
+  };
+  auto mfma_group = [&](int G) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int T = i % 4, kk = 2 * G + i / 4;
+      acc[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bq[kk], i < 4 ? zero : acc[T], 0, 0, 0);
+    }
+  };
+  auto scale_group = [&](float sc) {
+#pragma unroll
+    for (int T = 0; T < 4; ++T)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc, acc[T][v], y[T][v]);
+  };
+  decode2(wprev, 0);
+  if constexpr (MI == 0) {
+    decode2(wprev, 2);
+    read_group(0, 0);
+  }
 
   int stage = 0;  // t % 3
   for (int t = 0; t < steps; t += 4) {
@@ -314,71 +337,68 @@ __global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
       constexpr int J = decltype(jc)::value;
       const int tt = t + J;
       if (J >= 2 && tt > last) return;  // a last run of two steps
-      wait_vmcnt<wait_at(J)>();
-      __syncthreads();
-      // Iteration tt issues the activations of step tt+2 (into the stage
-      // step tt-1 used) in slots 0, 2, 4, 6, and at tt % 4 == 0 the packed
-      // words (slots 8, 10) and scale windows (slot 12) of steps tt+4 ..
-      // tt+7 (into the buffers steps tt-4 .. tt-1 used). Past the range end
-      // the last step (run) is fetched again into the same free places, so
-      // that every iteration issues the same transfers.
+      // Step tt issues the activations of step tt+2 (into the stage step
+      // tt-1 used) and, at tt % 4 == 0, the packed words and scale windows of
+      // steps tt+4 .. tt+7 (into the buffers steps tt-4 .. tt-1 used), all
+      // before its barrier. Past the range end the last step (run) is
+      // fetched again into the same free places, so that every step issues
+      // the same transfers.
       const int a_step = min(tt + 2, last), a_stage = stage == 0 ? 2 : stage - 1;
       const int w_step = min(tt + 4, last_run);
       const int buf = (tt >> 2) & 1;
-      // The next step's packed words (the last step reads its own again),
-      // decoded during this step; this step's scales; the fragments of slots 0..2.
+      const int next_stage = stage == 2 ? 0 : stage + 1;
+      auto transfers = [&]() {
+#pragma unroll
+        for (int i = 0; i < kAOps; ++i) issue_a1(a_step, a_stage, i);
+        if constexpr (J == 0) {
+          issue_w(w_step, buf ^ 1);
+          issue_s(w_step, buf ^ 1);
+        }
+      };
+      // The next step's packed words (the last step reads its own again) and this step's scales.
       const bool more = tt + 1 <= last;
       const u32x4_t wvn = J == 3 ? read_w(more ? buf ^ 1 : buf, more ? 0 : 3) : read_w(buf, J + 1);
       const uint32_t sdw = read_s(buf, J);
-      bf16x8_t af[16];  // by slot
-#pragma unroll
-      for (int s = 0; s < 3; ++s) af[s] = read_a(stage, slot_tile(s), slot_kk(s));
-      bf16x8_t bqn[4];
-      CodeTmp dt;
-      float sa = 0.0f, sb = 0.0f;
-      Unroll<0, 16>::run([&](auto sc_) {
-        constexpr int s = decltype(sc_)::value;
-        constexpr int T = slot_tile(s), kk = slot_kk(s);
-        if constexpr (s % 2 == 0 && s < 8) issue_a1(a_step, a_stage, s / 2);
-        if constexpr (J == 0 && s == 8) issue_w(w_step, buf ^ 1);
-        if constexpr (J == 0 && s == 12) issue_s(w_step, buf ^ 1);
-        if constexpr (s + 3 < 16) af[s + 3] = read_a(stage, slot_tile(s + 3), slot_kk(s + 3));
-        if constexpr (s == 1) {
-          sa = __uint_as_float(sdw << 16);
-          sb = __uint_as_float(sdw & 0xffff0000u);
-        }
-        acc[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bq[kk], kk % 2 == 0 ? zero : acc[T], 0, 0, 0);
-        // Scaling of the tiles whose group ended 3, 4 or 5 slots earlier.
-        Unroll<3, 6>::run([&](auto dc) {
-          constexpr int d = decltype(dc)::value;
-          constexpr int l = s - d, lm = (l + 16) % 16;
-          if constexpr (group_done(lm)) {
-            constexpr int ST = slot_tile(lm);
-            const float scale = l < 0 ? sb_prev : (lm < 8 ? sa : sb);
-#pragma unroll
-            for (int v = part_first(d); v < part_end(d); ++v) y[ST][v] = fmaf(scale, acc[ST][v], y[ST][v]);
-          }
-        });
-        // Decode of the next step's word w in slots 2+3w .. 4+3w.
-        if constexpr (s >= 2 && s < 14) {
-          constexpr int w = (s - 2) / 3, ph = (s - 2) % 3;
-          code_piece<ph>(wvn[w], dt, bqn[w]);
-        }
+      const float sa = __uint_as_float(sdw << 16), sb = __uint_as_float(sdw & 0xffff0000u);
+      if constexpr (MI == 0) {
+        mfma_group(0);
         __builtin_amdgcn_sched_barrier(0);
-      });
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) bq[kk] = bqn[kk];
-      sb_prev = sb;
-      stage = stage == 2 ? 0 : stage + 1;
+        read_group(stage, 1);
+        transfers();
+        decode2(wvn, 0);
+        scale_group(sa);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_group(1);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<mid_wait(J)>();
+        __syncthreads();
+        read_group(next_stage, 0);
+        decode2(wvn, 2);
+        scale_group(sb);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        read_group(stage, 0);
+        decode2(wprev, 2);
+        scale_group(sb_prev);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_group(0);
+        __builtin_amdgcn_sched_barrier(0);
+        read_group(stage, 1);
+        transfers();
+        decode2(wvn, 0);
+        scale_group(sa);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<mid_wait(J)>();
+        __syncthreads();
+        mfma_group(1);
+        __builtin_amdgcn_sched_barrier(0);
+        wprev = wvn;
+        sb_prev = sb;
+      }
+      stage = next_stage;
     });
   }
-  // The second group of the last step: tile 1's elements 11..15, tiles 2 and 3.
-#pragma unroll
-  for (int v = 11; v < 16; ++v) y[1][v] = fmaf(sb_prev, acc[1][v], y[1][v]);
-#pragma unroll
-  for (int T = 2; T < 4; ++T)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sb_prev, acc[T][v], y[T][v]);
+  if constexpr (MI == 1) scale_group(sb_prev);  // the second group of the last step
 
   // Bias term: y += sum over the range's groups of X_t[row][g] * b[col][g],
   // 16 groups per MFMA, in rounds of 64 groups: the tile's rows of the three
@@ -459,6 +479,16 @@ __global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
         }
     }
   });
+}
+
+__global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a[kAStages * kAStage];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_w[2 * kWBuf];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s[2 * kSBuf];
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 8) == 0)
+    re32_tile<0>(r, lds_a, lds_w, lds_s);
+  else
+    re32_tile<1>(r, lds_a, lds_w, lds_s);
 }
 
 }  // namespace
