@@ -337,12 +337,14 @@ hipError_t mfma_launch(const QmmProblem& p, const Launch& l) {
   // Above 128 rows (at 128 this kernel's 128-row tile wins: 38.1 against
   // 47.0 us for 128 x 14336 x 4096), 4-bit weights with bf16 parameters and
   // groups of 64 or 128 run the 8-wave GEMM of gemm_re.hip in its
-  // rounded-weight form where its K ranges are long enough; the pair kernel
+  // rounded-weight form where its K ranges are long enough, groups of 32 the
+  // 8-wave GEMM of gemm_re32.hip in its rounded-weight form; the pair kernel
   // takes the other 4-bit shapes.
   if (p.M > 128 && re_gemm_supports(p)) {
     hipError_t e = hipSuccess;
     if (re_gemm_launch(p, l, &e, true)) return e;
   }
+  if (p.M > 128 && re32_supports(p)) return re32_launch(p, l, true);
   if (p.M > 128 && pair_supports(p)) return pair_launch(p, l);
   hipStream_t stream = l.stream;
   TileArgs a;

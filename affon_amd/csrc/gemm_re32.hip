@@ -61,16 +61,18 @@ static_assert(kAOps == 4 && kWOps == 2 && kSOps == 1, "transfer counts assumed b
 static_assert(3 * kRows * kPlaneRound * 2 <= kAStages * kAStage, "a round of the three planes fits the ring");
 
 // vmcnt bound before the barrier of step t (j = t % 4), which sits between
-// the step's third and fourth phase. Before it, step t issues the
-// activations of step t+2 and, when t % 4 == 0, then the packed words and
-// scale windows of steps t+4 .. t+7; the prologue issues the words and
-// windows of steps 0..3, then the activations of steps 0 and 1. At the
+// the step's third and fourth phase (ROUNDED: between its two groups'
+// MFMAs). Before it, step t issues the activations of step t+2 and, when
+// t % 4 == 0, then the packed words and scale windows (ROUNDED: and bias
+// windows) of steps t+4 .. t+7; the prologue issues the words and windows
+// of steps 0..3, then the activations of steps 0 and 1. At the
 // barrier of step t the activations of step t+1 (issued by step t-1) must
 // have landed, for the fragment reads of step t+1 that follow it, and with
 // them everything issued before: the words and windows that the next steps
 // read at their start. In flight may stay the words and windows issued by
 // step t-1 (when t-1 = 0 mod 4) and every transfer of step t.
-constexpr int mid_wait(int j) { return kAOps + (j == 0 || j == 1 ? kWOps + kSOps : 0); }
+template <bool ROUNDED>
+constexpr int mid_wait(int j) { return kAOps + (j == 0 || j == 1 ? kWOps + (ROUNDED ? 2 : 1) * kSOps : 0); }
 
 // Slot (16-byte unit) of part `part` (0..7) in local column c's 128-byte
 // packed run.
@@ -153,6 +155,19 @@ __device__ __forceinline__ void code_piece(uint32_t w, CodeTmp& d, bf16x8_t& out
   }
 }
 
+// ROUNDED: the B operand bf16(s*q + b) of one packed word's eight codes in k
+// order (s carries the 2^9 of the FP8 reading of a code), the approximate
+// class's decoded weights.
+__device__ __forceinline__ bf16x8_t weights_rounded(uint32_t w, float s, float b) {
+  const uint32_t even = w & 0x0f0f0f0fu, odd = (w >> 4) & 0x0f0f0f0fu;
+  const f32x2_t e0 = __builtin_amdgcn_cvt_pk_f32_fp8(even, false), e1 = __builtin_amdgcn_cvt_pk_f32_fp8(even, true);
+  const f32x2_t o0 = __builtin_amdgcn_cvt_pk_f32_fp8(odd, false), o1 = __builtin_amdgcn_cvt_pk_f32_fp8(odd, true);
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{pack_bf16(fmaf(e0.x, s, b), fmaf(o0.x, s, b)),
+                                              pack_bf16(fmaf(e0.y, s, b), fmaf(o0.y, s, b)),
+                                              pack_bf16(fmaf(e1.x, s, b), fmaf(o1.x, s, b)),
+                                              pack_bf16(fmaf(e1.y, s, b), fmaf(o1.y, s, b))});
+}
+
 struct Re32Args {
   TileArgs t;
   const uint16_t* planes;  // [range][3][M][gr] bf16: X1, X2, X3 of every row and group
@@ -177,8 +192,16 @@ struct Re32Args {
 // and the next write of that stage (the activations of step t+3) is issued
 // by step t+1, after it. The packed words and scales a step reads at its
 // start are ordered against their transfers by earlier barriers the same way.
-template <int MI>
-__device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uint8_t* lds_w, uint8_t* lds_s) {
+//
+// ROUNDED: the approximate class instead. The B operands are the decoded
+// weights bf16(s*q + b) (each MFMA's 16 k lie in one group), the MFMAs
+// accumulate straight into y, the vector phases hold only the decode, and
+// there is no group-sum pre-pass or bias term. The biases stream in windows
+// beside the scales, and each step reads the next step's parameters with
+// its words.
+template <int MI, bool ROUNDED>
+__device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uint8_t* lds_w, uint8_t* lds_s,
+                                          uint8_t* lds_b) {
   const TileArgs& a = r.t;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -247,6 +270,12 @@ __device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uin
     const int d = min((s0 + step4) + s_d, row_dwords - 1);  // run (s0+step4)/4 starts at dword s0+step4
     dma4(a.s, s_off + 4 * d, lds_address(lds_s) + buf * kSBuf + 256 * wave);
   };
+  const uint32_t b_off =
+      static_cast<uint32_t>(min(n0 + sc, a.N - 1)) * static_cast<uint32_t>(a.bs0 * 2);
+  auto issue_b = [&](int step4, int buf) {  // ROUNDED: the bias windows, as the scale windows
+    const int d = min((s0 + step4) + s_d, row_dwords - 1);
+    dma4(a.b, b_off + 4 * d, lds_address(lds_b) + buf * kSBuf + 256 * wave);
+  };
 
   // A fragment (T, kk): local row 128*mi + 32*T + li, chunk 4*(kk/2) + 2*lh + kk%2.
   // The swizzle depends on the row only through li, so T adds 4096 bytes.
@@ -273,12 +302,16 @@ __device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uin
   auto read_s = [&](int buf, int sub) -> uint32_t {
     return *reinterpret_cast<const uint32_t*>(lds_s + buf * kSBuf + kSRun * wc + 4 * s_dword(wc, sub));
   };
+  auto read_b = [&](int buf, int sub) -> uint32_t {  // ROUNDED: both biases, as read_s
+    return *reinterpret_cast<const uint32_t*>(lds_b + buf * kSBuf + kSRun * wc + 4 * s_dword(wc, sub));
+  };
 
   // Prologue, in the issue order the waits count: packed words and scale
   // windows of steps 0..3; activations of steps 0 and 1. Then the B operands
   // of step 0 (the loop decodes them one step ahead).
   issue_w(0, 0);
   issue_s(0, 0);
+  if constexpr (ROUNDED) issue_b(0, 0);
 #pragma unroll
   for (int i = 0; i < kAOps; ++i) issue_a1(0, 0, i);
 #pragma unroll
@@ -286,173 +319,269 @@ __device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uin
   wait_vmcnt<kAOps>();  // the words and windows of steps 0..3, the activations of step 0
   __syncthreads();
 
-  f32x16_t y[4], acc[4];
+  f32x16_t y[4];
 #pragma unroll
   for (int T = 0; T < 4; ++T)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      y[T][v] = 0.0f;
-      acc[T][v] = 0.0f;  // mi = 1: the second group of "step -1" is scaled by 0 in the first step
-    }
-  const f32x16_t zero = {};
-  float sb_prev = 0.0f;  // mi = 1: second-group scale of the previous step
-  bf16x8_t bq[4];        // B operands of the step, by kk
-  bf16x8_t af[8];        // fragments of one MFMA phase: MFMA i is tile i % 4, kk 2G + i / 4
-  u32x4_t wprev = read_w(0, 0);  // mi = 1: the words whose second group the next first phase decodes
-  auto decode2 = [&](const u32x4_t& w, int kk0) {
-#pragma unroll
-    for (int k = kk0; k < kk0 + 2; ++k) {
-      CodeTmp d;
-      code_piece<0>(w[k], d, bq[k]);
-      code_piece<1>(w[k], d, bq[k]);
-      code_piece<2>(w[k], d, bq[k]);
-    }
-  };
-  auto read_group = [&](int stage, int G) {
+    for (int v = 0; v < 16; ++v) y[T][v] = 0.0f;
+  bf16x8_t bq[4];  // B operands of the step, by kk
+  // The fragments of one MFMA phase: MFMA i is tile i % 4, kk 2G + i / 4.
+  auto read_group = [&](bf16x8_t (&af)[8], int stage, int G) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) af[i] = read_a(stage, i % 4, 2 * G + i / 4);
   };
-  auto mfma_group = [&](int G) {
+
+  if constexpr (ROUNDED) {
+    // Software pipeline, the same for both waves of a SIMD: a step is its
+    // first group's eight MFMAs (accumulating into y), the barrier, its
+    // second group's eight. Each phase's fragments are read at the start of
+    // the phase before (the first group's of step t+1 right after the
+    // barrier of step t), and each phase decodes, one piece per MFMA, the two
+    // words the next phase but one needs: during the first group of step t
+    // the second group's words of step t, during the second group the first
+    // group's words of step t+1. The step's transfers are issued during its
+    // first group, before the barrier.
+    struct Params {
+      float s[2], b[2];  // per group of the step: scale (times 2^9), bias
+    };
+    auto params = [&](uint32_t sdw, uint32_t bdw) {
+      return Params{{__uint_as_float(sdw << 16) * 512.0f, __uint_as_float(sdw & 0xffff0000u) * 512.0f},
+                    {__uint_as_float(bdw << 16), __uint_as_float(bdw & 0xffff0000u)}};
+    };
+    // Piece PC (0..3) of the rounded decode of word w into B operand k.
+    struct Piece {
+      uint32_t even, odd;
+      f32x2_t e, o;
+      u32x4_t out;
+    };
+    auto piece = [&](auto pc, uint32_t w, float sc, float bi, Piece& d, int k) {
+      constexpr int PC = decltype(pc)::value;
+      if constexpr (PC == 0 || PC == 2) {
+        if constexpr (PC == 0) {
+          d.even = w & 0x0f0f0f0fu;
+          d.odd = (w >> 4) & 0x0f0f0f0fu;
+        }
+        d.e = __builtin_amdgcn_cvt_pk_f32_fp8(d.even, PC == 2);  // codes 0, 2 (4, 6)
+        d.o = __builtin_amdgcn_cvt_pk_f32_fp8(d.odd, PC == 2);   // codes 1, 3 (5, 7)
+      } else {
+        constexpr int o = PC == 1 ? 0 : 2;
+        d.out[o] = pack_bf16(fmaf(d.e.x, sc, bi), fmaf(d.o.x, sc, bi));
+        d.out[o + 1] = pack_bf16(fmaf(d.e.y, sc, bi), fmaf(d.o.y, sc, bi));
+        if constexpr (PC == 3) bq[k] = __builtin_bit_cast(bf16x8_t, d.out);
+      }
+    };
+    bf16x8_t afa[8], afb[8];  // fragments of the first and second group's phase
+    u32x4_t wcur = read_w(0, 0);
+    Params pc = params(read_s(0, 0), read_b(0, 0));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int T = i % 4, kk = 2 * G + i / 4;
-      acc[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bq[kk], i < 4 ? zero : acc[T], 0, 0, 0);
+    for (int k = 0; k < 2; ++k) bq[k] = weights_rounded(wcur[k], pc.s[0], pc.b[0]);
+    read_group(afa, 0, 0);
+
+    int stage = 0;  // t % 3
+    for (int t = 0; t < steps; t += 4) {
+      Unroll<0, 4>::run([&](auto jc) {
+        constexpr int J = decltype(jc)::value;
+        const int tt = t + J;
+        if (J >= 2 && tt > last) return;  // a last run of two steps
+        const int a_step = min(tt + 2, last), a_stage = stage == 0 ? 2 : stage - 1;
+        const int w_step = min(tt + 4, last_run);
+        const int buf = (tt >> 2) & 1;
+        const int next_stage = stage == 2 ? 0 : stage + 1;
+        // The next step's packed words and parameters (the last step reads its own again).
+        const bool more = tt + 1 <= last;
+        const int nb = J == 3 && more ? buf ^ 1 : buf, ns = J == 3 ? (more ? 0 : 3) : J + 1;
+        const u32x4_t wvn = read_w(nb, ns);
+        const Params pn = params(read_s(nb, ns), read_b(nb, ns));
+        read_group(afb, stage, 1);
+        Piece d;
+        Unroll<0, 8>::run([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          y[i % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afa[i], bq[i / 4], y[i % 4], 0, 0, 0);
+          // The activations first, then the words and windows: the counted
+          // waits assume this order.
+          if constexpr (i < kAOps) issue_a1(a_step, a_stage, i);
+          if constexpr (J == 0 && i == 4) issue_w(w_step, buf ^ 1);
+          if constexpr (J == 0 && i == 5) issue_s(w_step, buf ^ 1);
+          if constexpr (J == 0 && i == 6) issue_b(w_step, buf ^ 1);
+          piece(std::integral_constant<int, i % 4>{}, wcur[2 + i / 4], pc.s[1], pc.b[1], d, 2 + i / 4);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        wait_vmcnt<mid_wait<true>(J)>();
+        __syncthreads();
+        read_group(afa, next_stage, 0);
+        Unroll<0, 8>::run([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          y[i % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afb[i], bq[2 + i / 4], y[i % 4], 0, 0, 0);
+          piece(std::integral_constant<int, i % 4>{}, wvn[i / 4], pn.s[0], pn.b[0], d, i / 4);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        wcur = wvn;
+        pc = pn;
+        stage = next_stage;
+      });
     }
-  };
-  auto scale_group = [&](float sc) {
+    wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
+  } else {
+    f32x16_t acc[4];
 #pragma unroll
     for (int T = 0; T < 4; ++T)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc, acc[T][v], y[T][v]);
-  };
-  decode2(wprev, 0);
-  if constexpr (MI == 0) {
-    decode2(wprev, 2);
-    read_group(0, 0);
-  }
-
-  int stage = 0;  // t % 3
-  for (int t = 0; t < steps; t += 4) {
-    Unroll<0, 4>::run([&](auto jc) {
-      constexpr int J = decltype(jc)::value;
-      const int tt = t + J;
-      if (J >= 2 && tt > last) return;  // a last run of two steps
-      // Step tt issues the activations of step tt+2 (into the stage step
-      // tt-1 used) and, at tt % 4 == 0, the packed words and scale windows of
-      // steps tt+4 .. tt+7 (into the buffers steps tt-4 .. tt-1 used), all
-      // before its barrier. Past the range end the last step (run) is
-      // fetched again into the same free places, so that every step issues
-      // the same transfers.
-      const int a_step = min(tt + 2, last), a_stage = stage == 0 ? 2 : stage - 1;
-      const int w_step = min(tt + 4, last_run);
-      const int buf = (tt >> 2) & 1;
-      const int next_stage = stage == 2 ? 0 : stage + 1;
-      auto transfers = [&]() {
+      for (int v = 0; v < 16; ++v) acc[T][v] = 0.0f;  // mi = 1: the second group of "step -1" is scaled by 0
+    const f32x16_t zero = {};
+    float sb_prev = 0.0f;  // mi = 1: second-group scale of the previous step
+    bf16x8_t af[8];
+    u32x4_t wprev = read_w(0, 0);  // mi = 1: the words whose second group the next first phase decodes
+    auto decode2 = [&](const u32x4_t& w, int kk0) {
 #pragma unroll
-        for (int i = 0; i < kAOps; ++i) issue_a1(a_step, a_stage, i);
-        if constexpr (J == 0) {
-          issue_w(w_step, buf ^ 1);
-          issue_s(w_step, buf ^ 1);
-        }
-      };
-      // The next step's packed words (the last step reads its own again) and this step's scales.
-      const bool more = tt + 1 <= last;
-      const u32x4_t wvn = J == 3 ? read_w(more ? buf ^ 1 : buf, more ? 0 : 3) : read_w(buf, J + 1);
-      const uint32_t sdw = read_s(buf, J);
-      const float sa = __uint_as_float(sdw << 16), sb = __uint_as_float(sdw & 0xffff0000u);
-      if constexpr (MI == 0) {
-        mfma_group(0);
-        __builtin_amdgcn_sched_barrier(0);
-        read_group(stage, 1);
-        transfers();
-        decode2(wvn, 0);
-        scale_group(sa);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_group(1);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<mid_wait(J)>();
-        __syncthreads();
-        read_group(next_stage, 0);
-        decode2(wvn, 2);
-        scale_group(sb);
-        __builtin_amdgcn_sched_barrier(0);
-      } else {
-        read_group(stage, 0);
-        decode2(wprev, 2);
-        scale_group(sb_prev);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_group(0);
-        __builtin_amdgcn_sched_barrier(0);
-        read_group(stage, 1);
-        transfers();
-        decode2(wvn, 0);
-        scale_group(sa);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<mid_wait(J)>();
-        __syncthreads();
-        mfma_group(1);
-        __builtin_amdgcn_sched_barrier(0);
-        wprev = wvn;
-        sb_prev = sb;
+      for (int k = kk0; k < kk0 + 2; ++k) {
+        CodeTmp d;
+        code_piece<0>(w[k], d, bq[k]);
+        code_piece<1>(w[k], d, bq[k]);
+        code_piece<2>(w[k], d, bq[k]);
       }
-      stage = next_stage;
-    });
-  }
-  if constexpr (MI == 1) scale_group(sb_prev);  // the second group of the last step
-
-  // Bias term: y += sum over the range's groups of X_t[row][g] * b[col][g],
-  // 16 groups per MFMA, in rounds of 64 groups: the tile's rows of the three
-  // planes (plane t at 32 KiB * t of the activation ring, row r at 128 * r,
-  // 16-byte slot q at a_slot(r, q)) arrive by whole-line transfers; the
-  // lane's biases are read from global memory, zero past the range's groups
-  // (where the planes are zero too).
-  wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
-  __syncthreads();
-  {
-    const int rg = 2 * steps;  // groups of the range
-    const int g0 = split * rg;
-    const int rounds = r.gr / kPlaneRound;
-    const uint16_t* planes = r.planes + static_cast<int64_t>(split) * 3 * a.M * r.gr;
-    const uint8_t* brow = a.b + static_cast<int64_t>(min(n0 + wc, a.N - 1)) * a.bs0 * 2;
-    constexpr int kXOps = 3 * kRows / 8 / kWaves32;
-    for (int rd = 0; rd < rounds; ++rd) {
-      if (rd > 0) __syncthreads();  // every wave is done with the previous round's planes
+    };
+    auto mfma_group = [&](int G) {
 #pragma unroll
-      for (int ii = 0; ii < kXOps; ++ii) {
-        const int i = kXOps * wave + ii;  // plane i / 32, rows 8*(i%32) ..
-        const int pl = i / (kRows / 8), rgi = i % (kRows / 8);
-        const int row = min(m0 + 8 * rgi + (lane >> 3), a.M - 1);
-        const int q = (lane & 7) ^ (lane >> 3) ^ (rgi & 1);
-        load_lds<16>(planes + (static_cast<int64_t>(pl) * a.M + row) * r.gr + kPlaneRound * rd + 8 * q,
-                     lds_address(lds_a) + pl * (kRows * 128) + 1024 * rgi);
+      for (int i = 0; i < 8; ++i) {
+        const int T = i % 4, kk = 2 * G + i / 4;
+        acc[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bq[kk], i < 4 ? zero : acc[T], 0, 0, 0);
       }
-      u32x4_t bb[4];
+    };
+    auto scale_group = [&](float sc) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int T = 0; T < 4; ++T)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int gl = kPlaneRound * rd + 16 * c + 8 * lh + 2 * e;  // even, as rg and g0
-          bb[c][e] = gl < rg ? *reinterpret_cast<const uint32_t*>(brow + 2 * (g0 + gl)) : 0u;
-        }
-      wait_vmcnt<0>();
-      __syncthreads();
+        for (int v = 0; v < 16; ++v) y[T][v] = fmaf(sc, acc[T][v], y[T][v]);
+    };
+    decode2(wprev, 0);
+    if constexpr (MI == 0) {
+      decode2(wprev, 2);
+      read_group(af, 0, 0);
+    }
+
+    int stage = 0;  // t % 3
+    for (int t = 0; t < steps; t += 4) {
+      Unroll<0, 4>::run([&](auto jc) {
+        constexpr int J = decltype(jc)::value;
+        const int tt = t + J;
+        if (J >= 2 && tt > last) return;  // a last run of two steps
+        // Step tt issues the activations of step tt+2 (into the stage step
+        // tt-1 used) and, at tt % 4 == 0, the packed words and scale windows
+        // of steps tt+4 .. tt+7 (into the buffers steps tt-4 .. tt-1 used),
+        // all before its barrier. Past the range end the last step (run) is
+        // fetched again into the same free places, so that every step issues
+        // the same transfers.
+        const int a_step = min(tt + 2, last), a_stage = stage == 0 ? 2 : stage - 1;
+        const int w_step = min(tt + 4, last_run);
+        const int buf = (tt >> 2) & 1;
+        const int next_stage = stage == 2 ? 0 : stage + 1;
+        auto transfers = [&]() {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        u32x4_t xv[3][4];
-#pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-          for (int T = 0; T < 4; ++T) {
-            const int row = 128 * mi + 32 * T + li;
-            xv[pl][T] = *reinterpret_cast<const u32x4_t*>(lds_a + pl * (kRows * 128) + row * 128 +
-                                                          16 * a_slot(row, 2 * c + lh));
+          for (int i = 0; i < kAOps; ++i) issue_a1(a_step, a_stage, i);
+          if constexpr (J == 0) {
+            issue_w(w_step, buf ^ 1);
+            issue_s(w_step, buf ^ 1);
           }
+        };
+        // The next step's packed words (the last step reads its own again) and this step's scales.
+        const bool more = tt + 1 <= last;
+        const u32x4_t wvn = J == 3 ? read_w(more ? buf ^ 1 : buf, more ? 0 : 3) : read_w(buf, J + 1);
+        const uint32_t sdw = read_s(buf, J);
+        const float sa = __uint_as_float(sdw << 16), sb = __uint_as_float(sdw & 0xffff0000u);
+        if constexpr (MI == 0) {
+          mfma_group(0);
+          __builtin_amdgcn_sched_barrier(0);
+          read_group(af, stage, 1);
+          transfers();
+          decode2(wvn, 0);
+          scale_group(sa);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma_group(1);
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<mid_wait<false>(J)>();
+          __syncthreads();
+          read_group(af, next_stage, 0);
+          decode2(wvn, 2);
+          scale_group(sb);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          read_group(af, stage, 0);
+          decode2(wprev, 2);
+          scale_group(sb_prev);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma_group(0);
+          __builtin_amdgcn_sched_barrier(0);
+          read_group(af, stage, 1);
+          transfers();
+          decode2(wvn, 0);
+          scale_group(sa);
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<mid_wait<false>(J)>();
+          __syncthreads();
+          mfma_group(1);
+          __builtin_amdgcn_sched_barrier(0);
+          wprev = wvn;
+          sb_prev = sb;
+        }
+        stage = next_stage;
+      });
+    }
+    if constexpr (MI == 1) scale_group(sb_prev);  // the second group of the last step
+
+    // Bias term: y += sum over the range's groups of X_t[row][g] * b[col][g],
+    // 16 groups per MFMA, in rounds of 64 groups: the tile's rows of the three
+    // planes (plane t at 32 KiB * t of the activation ring, row r at 128 * r,
+    // 16-byte slot q at a_slot(r, q)) arrive by whole-line transfers; the
+    // lane's biases are read from global memory, zero past the range's groups
+    // (where the planes are zero too).
+    wait_vmcnt<0>();  // the loop's last transfers (re-fetches of the final step)
+    __syncthreads();
+    {
+      const int rg = 2 * steps;  // groups of the range
+      const int g0 = split * rg;
+      const int rounds = r.gr / kPlaneRound;
+      const uint16_t* planes = r.planes + static_cast<int64_t>(split) * 3 * a.M * r.gr;
+      const uint8_t* brow = a.b + static_cast<int64_t>(min(n0 + wc, a.N - 1)) * a.bs0 * 2;
+      constexpr int kXOps = 3 * kRows / 8 / kWaves32;
+      for (int rd = 0; rd < rounds; ++rd) {
+        if (rd > 0) __syncthreads();  // every wave is done with the previous round's planes
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
+        for (int ii = 0; ii < kXOps; ++ii) {
+          const int i = kXOps * wave + ii;  // plane i / 32, rows 8*(i%32) ..
+          const int pl = i / (kRows / 8), rgi = i % (kRows / 8);
+          const int row = min(m0 + 8 * rgi + (lane >> 3), a.M - 1);
+          const int q = (lane & 7) ^ (lane >> 3) ^ (rgi & 1);
+          load_lds<16>(planes + (static_cast<int64_t>(pl) * a.M + row) * r.gr + kPlaneRound * rd + 8 * q,
+                       lds_address(lds_a) + pl * (kRows * 128) + 1024 * rgi);
+        }
+        u32x4_t bb[4];
 #pragma unroll
-          for (int T = 0; T < 4; ++T)
-            y[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][T]),
-                                                           __builtin_bit_cast(bf16x8_t, bb[c]), y[T], 0, 0, 0);
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int gl = kPlaneRound * rd + 16 * c + 8 * lh + 2 * e;  // even, as rg and g0
+            bb[c][e] = gl < rg ? *reinterpret_cast<const uint32_t*>(brow + 2 * (g0 + gl)) : 0u;
+          }
+        wait_vmcnt<0>();
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4_t xv[3][4];
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+            for (int T = 0; T < 4; ++T) {
+              const int row = 128 * mi + 32 * T + li;
+              xv[pl][T] = *reinterpret_cast<const u32x4_t*>(lds_a + pl * (kRows * 128) + row * 128 +
+                                                            16 * a_slot(row, 2 * c + lh));
+            }
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+              y[T] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, xv[pl][T]),
+                                                             __builtin_bit_cast(bf16x8_t, bb[c]), y[T], 0, 0, 0);
+        }
       }
     }
   }
@@ -481,14 +610,16 @@ __device__ __forceinline__ void re32_tile(const Re32Args& r, uint8_t* lds_a, uin
   });
 }
 
+template <bool ROUNDED>
 __global__ __launch_bounds__(kThreads32) void qgemm_re32_kernel(Re32Args r) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_a[kAStages * kAStage];
   __shared__ __attribute__((aligned(16))) uint8_t lds_w[2 * kWBuf];
   __shared__ __attribute__((aligned(16))) uint8_t lds_s[2 * kSBuf];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b[ROUNDED ? 2 * kSBuf : 16];  // ROUNDED: bias windows
   if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 8) == 0)
-    re32_tile<0>(r, lds_a, lds_w, lds_s);
+    re32_tile<0, ROUNDED>(r, lds_a, lds_w, lds_s, lds_b);
   else
-    re32_tile<1>(r, lds_a, lds_w, lds_s);
+    re32_tile<1, ROUNDED>(r, lds_a, lds_w, lds_s, lds_b);
 }
 
 }  // namespace
@@ -513,7 +644,7 @@ bool re32_supports(const QmmProblem& p) {
   return true;
 }
 
-hipError_t re32_launch(const QmmProblem& p, const Launch& l) {
+hipError_t re32_launch(const QmmProblem& p, const Launch& l, bool rounded) {
   Re32Args r;
   TileArgs& a = r.t;
   a.x = reinterpret_cast<const uint16_t*>(p.x);
@@ -540,19 +671,29 @@ hipError_t re32_launch(const QmmProblem& p, const Launch& l) {
   const int range_groups = 2 * a.split_steps;
   r.gr = padded_groups(range_groups);
   const size_t partial_bytes = splits > 1 ? static_cast<size_t>(splits) * p.M * p.N * 4 : 0;
-  const size_t plane_bytes = static_cast<size_t>(splits) * 3 * p.M * r.gr * 2;
+  // ROUNDED: no group-sum planes.
+  const size_t plane_bytes = rounded ? 0 : static_cast<size_t>(splits) * 3 * p.M * r.gr * 2;
   const size_t total = ((partial_bytes + 255) & ~size_t(255)) + plane_bytes;
-  uint8_t* scratch = static_cast<uint8_t*>(l.scratch(total));
-  if (scratch == nullptr) return hipErrorOutOfMemory;  // nothing launched (l.fixed_short says why, if fixed)
+  uint8_t* scratch = nullptr;
+  if (total > 0) {
+    scratch = static_cast<uint8_t*>(l.scratch(total));
+    if (scratch == nullptr) return hipErrorOutOfMemory;  // nothing launched (l.fixed_short says why, if fixed)
+  }
   a.partial = splits > 1 ? reinterpret_cast<float*>(scratch) : nullptr;
-  r.planes = reinterpret_cast<const uint16_t*>(scratch + ((partial_bytes + 255) & ~size_t(255)));
+  r.planes = rounded ? nullptr : reinterpret_cast<const uint16_t*>(scratch + ((partial_bytes + 255) & ~size_t(255)));
 
-  const int64_t entries = static_cast<int64_t>(p.M) * splits * r.gr;
-  hipLaunchKernelGGL(re32_group_sums_kernel, dim3(static_cast<unsigned>((entries + 255) / 256)), dim3(256), 0,
-                     l.stream, a.x, a.xs0, a.M, range_groups, r.gr, splits, const_cast<uint16_t*>(r.planes));
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(qgemm_re32_kernel, dim3(tiles * splits), dim3(kThreads32), 0, l.stream, r);
+  hipError_t e = hipSuccess;
+  if (!rounded) {
+    const int64_t entries = static_cast<int64_t>(p.M) * splits * r.gr;
+    hipLaunchKernelGGL(re32_group_sums_kernel, dim3(static_cast<unsigned>((entries + 255) / 256)), dim3(256), 0,
+                       l.stream, a.x, a.xs0, a.M, range_groups, r.gr, splits, const_cast<uint16_t*>(r.planes));
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (rounded)
+    hipLaunchKernelGGL(qgemm_re32_kernel<true>, dim3(tiles * splits), dim3(kThreads32), 0, l.stream, r);
+  else
+    hipLaunchKernelGGL(qgemm_re32_kernel<false>, dim3(tiles * splits), dim3(kThreads32), 0, l.stream, r);
   e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   return launch_reduce(a, l.stream);

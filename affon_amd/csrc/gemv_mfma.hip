@@ -485,7 +485,7 @@ hipError_t gemv_mfma_launch(const QmmProblem& p, const Launch& l) {
     hipError_t e = hipSuccess;
     if (re_gemm_launch(p, l, &e, false)) return e;
   }
-  if (!tiled_supports(p)) return re32_launch(p, l);
+  if (!tiled_supports(p)) return re32_launch(p, l, false);
   return tiled_launch(p, nullptr, 0, l);
 }
 

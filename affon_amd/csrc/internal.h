@@ -118,9 +118,11 @@ bool re_gemm_launch(const QmmProblem& p, const Launch& l, hipError_t* status, bo
 
 // The reassociated prefill GEMM for groups of 32 (gemm_re32.hip), which
 // gemv_mfma_launch runs for tall activations whose groups the group-scaling
-// GEMM and the LDS-tiled kernel do not take.
+// GEMM and the LDS-tiled kernel do not take. `rounded`: the same kernel in
+// the approximate class (decoded weights rounded to bf16), which mfma_launch
+// runs for such shapes past 128 rows.
 bool re32_supports(const QmmProblem& p);
-hipError_t re32_launch(const QmmProblem& p, const Launch& l);
+hipError_t re32_launch(const QmmProblem& p, const Launch& l, bool rounded);
 
 bool mfma_supports(const QmmProblem& p);
 hipError_t mfma_launch(const QmmProblem& p, const Launch& l);

@@ -16,7 +16,11 @@ Checks against f64 products computed here:
     approximate GEMM on the same inputs violates the bound;
   * the fused output-bias and SiLU-gate epilogues, repeat determinism, and
     both orientations of the 2048-row stress shape on sampled columns
-    including the first and last column tiles, against f64.
+    including the first and last column tiles, against f64;
+  * the same kernel's approximate form (decoded weights rounded to bf16,
+    the approximate policy's path past 128 rows): bit-exact where every
+    decoded weight is exact in bf16, and within the bf16-product tolerance
+    of the oracle and of the default policy on seeded inputs.
 """
 import numpy as np
 import pytest
@@ -162,3 +166,53 @@ def test_g32_prefill_stress_full_size(session):
         ratio = accuracy_ratio(out, xt.storage(), packed.storage(), scales.storage(), biases.storage(), 32, cols)
         assert ratio <= 2.0 ** -18, f"{N}x{K}: worst error {ratio:.3g} of sum|x*w|"
         del packed, scales, biases, xt, out
+
+# ---- the same kernel in the approximate class (implementation "mfma", past 128 rows) ----
+
+MFMA = "rocm_quantized_matmul.mfma"
+
+# (M, N, K): one row tile, 16 column tiles, four K ranges; partial row and
+# column tiles, eight K ranges; 5 row tiles over one range; one range of 68
+# steps (17 packed-word runs). The approximate candidate takes K in whole
+# multiples of 256, so no last run of two steps occurs here.
+ROUNDED_SHAPES = [(256, 2048, 2048), (300, 200, 4096), (1100, 256, 768), (600, 300, 4352)]
+
+
+@pytest.mark.parametrize("shape", ROUNDED_SHAPES, ids=lambda s: "m{}_n{}_k{}".format(*s))
+def test_g32_rounded_prefill_exact(session, shape, rng):
+    """Under the approximate policy the kernel rounds each decoded weight
+    s*q + b to bf16 (per group of 32). Power-of-two scales, integer biases in
+    [-2, 2] and codes below 16 keep every decoded weight exact in bf16
+    (multiples of 1/8 below 18), so with integer activations in [-3, 3] every
+    partial sum is a multiple of 1/8 below 2^18 and the output must equal the
+    f64 product bit for bit."""
+    from tests.test_gpu_prefill_reassociated import exact_operands as rounded_operands
+    M, N, K = shape
+    x, q, s, b = rounded_operands(rng, M, N, K, 32)
+    xt = upload(session, storage(x, "bf16"), "bf16")
+    wt = upload(session, pack_codes(q, 4), "u32")
+    st, bt = upload(session, storage(s, "bf16"), "bf16"), upload(session, storage(b, "bf16"), "bf16")
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=32, policy="approximate") == MFMA
+    out = session.empty("f32", (M, N))
+    A.quantized_matmul_into(out, xt, wt, st, bt, bits=4, group_size=32, implementation="mfma",
+                            policy="approximate")
+    cols = np.unique(np.concatenate([np.arange(min(N, 160)), np.linspace(0, N - 1, 96).astype(int)]))
+    np.testing.assert_array_equal(out.numpy()[:, cols], product_f64(x, q, s, b, 32, cols).astype(np.float32),
+                                  err_msg=f"{shape}")
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 1024, 4096), (300, 640, 8192)])
+def test_g32_rounded_prefill_against_oracle_and_default(session, M, N, K):
+    """Seeded inputs: the approximate policy's output within the bf16-product
+    tolerance of the oracle (rtol 1e-2, atol 1e-2 * rms) and of the default
+    policy's output on every element."""
+    from tests.helpers import assert_bf16_product_close, oracle_columns
+    x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=53)
+    xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+    assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=32, policy="approximate") == MFMA
+    approx = session.empty("f32", (M, N))
+    A.quantized_matmul_into(approx, xt, wt, st, bt, bits=4, group_size=32, policy="approximate")
+    default = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=32).numpy()
+    cols = np.unique(np.linspace(0, N - 1, 256).astype(int))
+    assert_bf16_product_close(approx.numpy()[:, cols], oracle_columns(x, packed, s, b, 4, 32, cols))
+    assert_bf16_product_close(approx.numpy(), default)
