@@ -222,3 +222,45 @@ def test_reassociated_gemm_declines_offsets_past_31_bits():
         d = make_desc(M=M, K=K, N=N)
         d.packed = _view(4096, (N, words), (ws0, 1), _native.U32)
         assert kernel_supports(d, "gemm_re") == accepted, ws0
+
+
+def test_group32_gemm_guard():
+    """The group-32 prefill GEMM (both classes) takes 4-bit codes with bf16
+    activations and parameters, groups of 32, K a multiple of 128, and feeds
+    its transfers 32-bit byte offsets from a scalar base: the last activation
+    row, packed-word row and parameter rows must start below 2^31 bytes.
+    Strided views (no memory is touched on the CPU) put them just below and
+    just at the bound."""
+    K, N, M = 4096, 256, 512
+    assert kernel_supports(make_desc(M=M, K=K, N=N, group=32), "gemm_re32") == 1
+    assert kernel_supports(make_desc(M=M, K=K, N=N, group=64), "gemm_re32") == 0
+    assert kernel_supports(make_desc(M=M, K=K + 64, N=N, group=32), "gemm_re32") == 0
+    assert kernel_supports(make_desc(M=M, K=K, N=N, group=32, p_dtype=_native.F32), "gemm_re32") == 0
+    assert kernel_supports(make_desc(M=M, K=K, N=N, bits=8, group=32), "gemm_re32") == 0
+    limit = 2**31
+    for xs0, accepted in ((limit // (2 * M) - 8, 1), (limit // (2 * M), 0)):
+        d = make_desc(M=M, K=K, N=N, group=32)
+        d.input = _view(4096, (M, K), (xs0, 1), _native.BF16)
+        assert kernel_supports(d, "gemm_re32") == accepted, xs0
+    words = K // 8
+    for ws0, accepted in ((limit // (4 * N) - 4, 1), (limit // (4 * N), 0)):
+        d = make_desc(M=M, K=K, N=N, group=32)
+        d.packed = _view(4096, (N, words), (ws0, 1), _native.U32)
+        assert kernel_supports(d, "gemm_re32") == accepted, ws0
+    groups = K // 32
+    for ss0, accepted in ((limit // (2 * N) - 2, 1), (limit // (2 * N), 0)):
+        for field in ("scales", "biases"):
+            d = make_desc(M=M, K=K, N=N, group=32)
+            setattr(d, field, _view(4096, (N, groups), (ss0, 1), _native.BF16))
+            assert kernel_supports(d, "gemm_re32") == accepted, (field, ss0)
+
+
+def test_group32_prefill_selection():
+    """Groups of 32 past 128 rows: the approximate candidate under the
+    approximate policy (whose 4-bit prefill runs the group-32 GEMM's
+    rounded-weight form), the decode-batch candidate under the default
+    policy (which runs its exact-code form)."""
+    d = make_desc(M=512, K=4096, N=1024, group=32, policy=_native.APPROXIMATE)
+    assert select(d) == (0, "rocm_quantized_matmul.mfma")
+    d = make_desc(M=512, K=4096, N=1024, group=32, policy=_native.BACKEND_EQUIVALENT)
+    assert select(d) == (0, "rocm_quantized_matmul.gemv_mfma")
