@@ -18,22 +18,22 @@ from tests.helpers import HipRuntime
 pytestmark = pytest.mark.gpu
 
 
-def problem(session, M, N, K, seed):
+def problem(session, M, N, K, seed, group=64):
     rng = np.random.default_rng(seed)
     x = session.from_bytes(A.core.bf16_bits(rng.standard_normal((M, K)).astype(np.float32)), A.TensorSpec.bf16((M, K)))
     w = session.from_bytes(rng.integers(0, 1 << 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32),
                            A.TensorSpec.u32((N, K // 8)))
-    s = session.from_bytes(A.core.bf16_bits((0.008 + 0.004 * rng.random((N, K // 64))).astype(np.float32)),
-                           A.TensorSpec.bf16((N, K // 64)))
-    b = session.from_bytes(A.core.bf16_bits((-0.06 + 0.02 * rng.random((N, K // 64))).astype(np.float32)),
-                           A.TensorSpec.bf16((N, K // 64)))
+    s = session.from_bytes(A.core.bf16_bits((0.008 + 0.004 * rng.random((N, K // group))).astype(np.float32)),
+                           A.TensorSpec.bf16((N, K // group)))
+    b = session.from_bytes(A.core.bf16_bits((-0.06 + 0.02 * rng.random((N, K // group))).astype(np.float32)),
+                           A.TensorSpec.bf16((N, K // group)))
     return x, w, s, b
 
 
-def run(session, entry, operands, policy):
+def run(session, entry, operands, policy, group=64):
     x, w, s, b = operands
     out = session.tensor(np.full((x.shape[0], w.shape[0]), 7.0, np.float32))
-    desc = ops._descriptor(x, w, s, b, 4, 64, out, "auto", policy)
+    desc = ops._descriptor(x, w, s, b, 4, group, out, "auto", policy)
     status = getattr(_native.load(), entry)(session._handle, ctypes.byref(desc))
     message = _native.last_error()  # before the synchronize clears it
     session.synchronize()
@@ -50,13 +50,18 @@ def test_noalloc_matches_allocating_entry_point():
             # sums (32 MiB) plus its per-group activation sums (768 KiB)
             ((512, 4096, 14336), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma"),
             # a smaller decode batch with split K, reusing what the first call left in the array
-            ((16, 4096, 4096), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma"),
+            ((16, 4096, 4096), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma", 64),
+            # groups of 32 on the group-32 GEMM, eight K ranges: exact codes with their per-group
+            # activation sums (16 MiB + 1.5 MiB), then rounded weights (16 MiB)
+            ((512, 1024, 4096), "backend_equivalent", "rocm_quantized_matmul.gemv_mfma", 32),
+            ((512, 1024, 4096), "approximate", "rocm_quantized_matmul.mfma", 32),
         ]
-        for (M, N, K), policy, impl in cases:
-            operands = problem(session, M, N, K, seed=M + N)
-            assert A.selected_implementation(*operands, bits=4, group_size=64, policy=policy) == impl
-            want_status, want, _ = run(session, "affon_rocm_quantized_matmul", operands, policy)
-            got_status, got, message = run(session, "affon_rocm_quantized_matmul_noalloc", operands, policy)
+        for (M, N, K), policy, impl, *grp in cases:
+            group = grp[0] if grp else 64
+            operands = problem(session, M, N, K, seed=M + N, group=group)
+            assert A.selected_implementation(*operands, bits=4, group_size=group, policy=policy) == impl
+            want_status, want, _ = run(session, "affon_rocm_quantized_matmul", operands, policy, group)
+            got_status, got, message = run(session, "affon_rocm_quantized_matmul_noalloc", operands, policy, group)
             assert want_status == 0 and got_status == 0, message
             assert np.isfinite(got).all()
             np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=f"{M}x{N}x{K}")
