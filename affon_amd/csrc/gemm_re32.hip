@@ -34,6 +34,11 @@
 // four steps at a time (128 bytes per column) and the matching 16-byte scale
 // windows (eight groups per column) into two buffers, four steps ahead. One
 // barrier per step orders the shared tiles.
+//
+// With ROUNDED the same frame runs the approximate class (the mfma
+// candidate's path for these shapes past 128 rows): decoded weights
+// bf16(s*q + b) in the B operands, MFMAs accumulating into y, no group sums
+// or bias term; bias windows stream beside the scale windows.
 
 #include "lds_pipeline.h"
 
@@ -195,8 +200,9 @@ struct Re32Args {
 //
 // ROUNDED: the approximate class instead. The B operands are the decoded
 // weights bf16(s*q + b) (each MFMA's 16 k lie in one group), the MFMAs
-// accumulate straight into y, the vector phases hold only the decode, and
-// there is no group-sum pre-pass or bias term. The biases stream in windows
+// accumulate straight into y, and there is no group-sum pre-pass or bias
+// term. Both waves of a SIMD run the same software pipeline (at its loop
+// below) instead of the opposite phases. The biases stream in windows
 // beside the scales, and each step reads the next step's parameters with
 // its words.
 template <int MI, bool ROUNDED>
