@@ -205,13 +205,16 @@ def test_g32_rounded_prefill_exact(session, shape, rng):
 def test_g32_rounded_prefill_against_oracle_and_default(session, M, N, K):
     """Seeded inputs: the approximate policy's output within the bf16-product
     tolerance of the oracle (rtol 1e-2, atol 1e-2 * rms) and of the default
-    policy's output on every element."""
+    policy's output on every element; a second run is bit-identical."""
     from tests.helpers import assert_bf16_product_close, oracle_columns
     x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=53)
     xt, wt, st, bt = (upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
     assert A.selected_implementation(xt, wt, st, bt, bits=4, group_size=32, policy="approximate") == MFMA
     approx = session.empty("f32", (M, N))
     A.quantized_matmul_into(approx, xt, wt, st, bt, bits=4, group_size=32, policy="approximate")
+    again = session.empty("f32", (M, N))
+    A.quantized_matmul_into(again, xt, wt, st, bt, bits=4, group_size=32, policy="approximate")
+    np.testing.assert_array_equal(again.numpy(), approx.numpy())
     default = A.quantized_matmul(xt, wt, st, bt, bits=4, group_size=32).numpy()
     cols = np.unique(np.linspace(0, N - 1, 256).astype(int))
     assert_bf16_product_close(approx.numpy()[:, cols], oracle_columns(x, packed, s, b, 4, 32, cols))
