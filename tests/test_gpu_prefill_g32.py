@@ -19,8 +19,9 @@ Checks against f64 products computed here:
     including the first and last column tiles, against f64;
   * the same kernel's approximate form (decoded weights rounded to bf16,
     the approximate policy's path past 128 rows): bit-exact where every
-    decoded weight is exact in bf16, and within the bf16-product tolerance
-    of the oracle and of the default policy on seeded inputs.
+    decoded weight is exact in bf16, within the bf16-product tolerance of
+    the oracle and of the default policy on seeded inputs, repeat
+    determinism, and its output-bias and SiLU-gate epilogues.
 """
 import numpy as np
 import pytest
@@ -219,3 +220,36 @@ def test_g32_rounded_prefill_against_oracle_and_default(session, M, N, K):
     cols = np.unique(np.linspace(0, N - 1, 256).astype(int))
     assert_bf16_product_close(approx.numpy()[:, cols], oracle_columns(x, packed, s, b, 4, 32, cols))
     assert_bf16_product_close(approx.numpy(), default)
+
+
+def test_g32_rounded_prefill_epilogues(session, rng):
+    """The rounded form's output bias (f32, bf16) and SiLU-gated product under
+    the approximate policy, eight K ranges (the reduction applies them): the
+    bias bit-exact against the plain product plus the same f32 add, the gate
+    within 6 ulp of silu(g) * u in f64."""
+    M, N, K = 512, 1024, 4096
+    x, gp, gs, gb = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=59)
+    _, upk, us, ub = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=61)
+    xt = upload(session, x, "bf16")
+    gate = tuple(upload(session, a, dtype_of(a)) for a in (gp, gs, gb))
+    up = tuple(upload(session, a, dtype_of(a)) for a in (upk, us, ub))
+    assert A.selected_implementation(xt, *gate, bits=4, group_size=32, policy="approximate") == MFMA
+    g = session.empty("f32", (M, N))
+    A.quantized_matmul_into(g, xt, *gate, bits=4, group_size=32, policy="approximate")
+    u = session.empty("f32", (M, N))
+    A.quantized_matmul_into(u, xt, *up, bits=4, group_size=32, policy="approximate")
+    g, u = g.numpy(), u.numpy()
+    for bias_dtype in ("f32", "bf16"):
+        bias_values = rng.standard_normal(N).astype(np.float32)
+        bias = storage(bias_values, "bf16") if bias_dtype == "bf16" else bias_values
+        fused = A.quantized_linear(xt, *gate, upload(session, bias, bias_dtype), bits=4, group_size=32,
+                                   policy="approximate").numpy()
+        np.testing.assert_array_equal(fused, (g + widened(bias).astype(np.float32)).astype(np.float32),
+                                      err_msg=bias_dtype)
+    fused = A.quantized_silu_gate(xt, gate, up, bits=4, group_size=32, policy="approximate").numpy()
+    g64 = g.astype(np.float64)
+    with np.errstate(over="ignore"):
+        expected = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
+    bound = 6 * np.spacing(np.abs(expected).astype(np.float32)).astype(np.float64) + 1e-30
+    err = np.abs(fused.astype(np.float64) - expected)
+    assert np.all(err <= bound), f"worst {float(err.max())}"
