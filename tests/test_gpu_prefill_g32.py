@@ -21,7 +21,9 @@ Checks against f64 products computed here:
     the approximate policy's path past 128 rows): bit-exact where every
     decoded weight is exact in bf16, within the bf16-product tolerance of
     the oracle and of the default policy on seeded inputs, repeat
-    determinism, and its output-bias and SiLU-gate epilogues.
+    determinism, and its output-bias and SiLU-gate epilogues;
+  * both forms captured into a HIP graph and replayed, bit-identical to the
+    eager results.
 """
 import numpy as np
 import pytest
@@ -253,3 +255,55 @@ def test_g32_rounded_prefill_epilogues(session, rng):
     bound = 6 * np.spacing(np.abs(expected).astype(np.float32)).astype(np.float64) + 1e-30
     err = np.abs(fused.astype(np.float64) - expected)
     assert np.all(err <= bound), f"worst {float(err.max())}"
+
+
+def test_g32_graph_replay(session):
+    """Both forms of the group-32 GEMM (the default policy's exact codes with
+    its group-sum pre-pass, the approximate policy's rounded weights, each
+    over eight K ranges and the reduction) captured into one HIP graph on
+    the session stream, after eager calls sized the workspace, and replayed
+    three times. Between replays an eager call of another shape leaves other
+    contents in the workspace and the outputs are cleared; every replay
+    reproduces the eager results bit for bit."""
+    import ctypes
+
+    from affon_amd import _native, ops
+    from tests.helpers import HipRuntime
+    hip = HipRuntime()
+    lib = _native.load()
+    # Each descriptor holds raw device pointers: its operands stay referenced
+    # here for as long as the descriptor (and the graph) is used.
+    calls = []
+    for (M, N, K), policy in (((512, 1024, 4096), "backend_equivalent"), ((300, 640, 8192), "approximate")):
+        x, packed, s, b = seeded_problem(M, N, K, 4, 32, "bf16", "bf16", seed=M + 3)
+        operands = tuple(upload(session, a, dtype_of(a)) for a in (x, packed, s, b))
+        out = session.tensor(np.full((M, N), 7.0, np.float32))
+        desc = ops._descriptor(*operands, 4, 32, out, "auto", policy)
+        calls.append((desc, out, operands))
+    eager = []
+    for desc, out, _ in calls:
+        assert lib.affon_rocm_quantized_matmul(session._handle, ctypes.byref(desc)) == 0, _native.last_error()
+        session.synchronize()
+        eager.append(out.numpy().copy())
+
+    def enqueue():
+        for desc, _, _ in calls:
+            assert lib.affon_rocm_quantized_matmul(session._handle, ctypes.byref(desc)) == 0, _native.last_error()
+
+    graph = hip.capture(session.stream, enqueue)
+    try:
+        ox, op, osc, ob = seeded_problem(256, 512, 4096, 4, 32, "bf16", "bf16", seed=71)
+        other = tuple(upload(session, a, dtype_of(a)) for a in (ox, op, osc, ob))
+        for i in range(3):
+            A.quantized_matmul(*other, bits=4, group_size=32)
+            for _, out, _ in calls:
+                zeros = np.zeros(out.shape, np.float32)
+                _native.check(lib.affon_rocm_memcpy_h2d(session._handle, out.data_ptr, zeros.ctypes.data,
+                                                        zeros.nbytes), "clear")
+            session.synchronize()
+            hip.replay(session.stream, graph)
+            for (_, out, _), want in zip(calls, eager):
+                np.testing.assert_array_equal(out.numpy().view(np.uint32), want.view(np.uint32),
+                                              err_msg=f"replay {i}, output {out.shape}")
+    finally:
+        hip.destroy(graph)
