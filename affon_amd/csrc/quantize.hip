@@ -35,55 +35,87 @@ __device__ __forceinline__ void store_param(void* base, int64_t index, float v, 
     static_cast<float*>(base)[index] = v;
 }
 
-__device__ __forceinline__ uint32_t code(float w, float s, float b, float max_q) {
-  if (s == 0.0f) return 0u;
-  float r = rintf((w - b) / s);
-  if (!(r >= 0.0f)) r = 0.0f;
-  if (r > max_q) r = max_q;
-  return static_cast<uint32_t>(r);
+__device__ __forceinline__ uint32_t clamp_code(float r, float max_q) {
+  // fmaxf returns the other operand for a NaN: NaN and negative values give 0.
+  return static_cast<uint32_t>(fminf(fmaxf(r, 0.0f), max_q));
 }
 
-// One thread per packed word; the g/P threads of a group sit in one aligned
-// lane group of size WPG (a power of two <= 64) and combine min/max with
+__device__ __forceinline__ uint32_t code(float w, float s, float b, float max_q) {
+  if (s == 0.0f) return 0u;
+  return clamp_code(rintf((w - b) / s), max_q);
+}
+
+// One thread per packed word; the WPG = g/P threads of a group sit in one
+// aligned lane group (WPG a power of two <= 64) and combine min/max with
 // butterfly shuffles. Reads are contiguous per thread and across lanes.
-template <int BITS, typename WT>
-__global__ __launch_bounds__(256) void quantize_words_kernel(const uint8_t* weights, int64_t total_words, int wpg,
+//
+// The codes clamp(rint((w - b) / s)) take one division per thread instead of
+// one per value. With inv = 1/s correctly rounded (s in [2^-125, 2^125], so
+// inv is normal) and qt = (w - b) * inv rounded, qt lies within
+// 1.5 * 2^-23 * |q| of the exact quotient q, and the correctly rounded
+// quotient RN(q) within 2^-24 * |q|. While |qt| <= 2^BITS, both lie within
+// kNear = 2^BITS * 2^-20 of each other, so when qt is farther than kNear from
+// every half-integer, rint gives the same integer for both. Past that range
+// both clamp to the same end code, and NaN and infinite quotients clamp alike.
+// A thread with a value nearer a half-integer, or a scale outside the range
+// (zero, subnormal, huge, NaN), recomputes its word with the division.
+template <int BITS, typename WT, int WPG>
+__global__ __launch_bounds__(256) void quantize_words_kernel(const uint8_t* weights, int64_t total_words,
                                                              uint32_t* packed, void* scales, void* biases,
                                                              bool bf16_params) {
   constexpr int P = 32 / BITS;
   constexpr float kMaxQ = static_cast<float>((1u << BITS) - 1u);
+  constexpr float kNear = static_cast<float>(1u << BITS) * 0x1p-20f;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const bool active = t < total_words;
   // Threads past the end belong to lane groups that hold no real word
-  // (total_words is a multiple of wpg), so they may read any valid word.
+  // (total_words is a multiple of WPG), so they may read any valid word.
   const int64_t tt = active ? t : total_words - 1;
   float v[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) v[i] = load_weight<WT>(weights, tt * P + i);
+  // The group's min / max as a comparison scan from its first value gives
+  // them: NaN when that value is NaN, otherwise over the values that are not
+  // NaN (fminf / fmaxf skip a NaN operand).
   float mn = v[0], mx = v[0];
 #pragma unroll
   for (int i = 1; i < P; ++i) {
-    mn = v[i] < mn ? v[i] : mn;
-    mx = v[i] > mx ? v[i] : mx;
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
   }
-  for (int offset = 1; offset < wpg; offset <<= 1) {
-    const float omn = __shfl_xor(mn, offset);
-    const float omx = __shfl_xor(mx, offset);
-    mn = omn < mn ? omn : mn;
-    mx = omx > mx ? omx : mx;
+#pragma unroll
+  for (int offset = 1; offset < WPG; offset <<= 1) {
+    mn = fminf(mn, __shfl_xor(mn, offset));
+    mx = fmaxf(mx, __shfl_xor(mx, offset));
   }
+  const float first = __shfl(v[0], 0, WPG);
+  if (first != first) mn = mx = first;
   const float scale = (mx - mn) / kMaxQ + 0.0f;
   const float bias = mn + 0.0f;
   const float s = stored_param(scale, bf16_params);
   const float b = stored_param(bias, bf16_params);
   if (!active) return;
-  if ((t & (wpg - 1)) == 0) {
-    store_param(scales, t / wpg, scale, bf16_params);
-    store_param(biases, t / wpg, bias, bf16_params);
+  if ((t & (WPG - 1)) == 0) {
+    store_param(scales, t / WPG, scale, bf16_params);
+    store_param(biases, t / WPG, bias, bf16_params);
+  }
+  const float inv = 1.0f / s;
+  float d[P], r[P];
+  float worst = 0.0f;  // the largest |qt - rint(qt)| of the word
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    d[i] = v[i] - b;
+    const float qt = d[i] * inv;
+    r[i] = rintf(qt);
+    worst = fmaxf(worst, fabsf(qt - r[i]));
+  }
+  if (!(s >= 0x1p-125f && s <= 0x1p125f) || worst >= 0.5f - kNear) {
+#pragma unroll
+    for (int i = 0; i < P; ++i) r[i] = s == 0.0f ? 0.0f : rintf(d[i] / s);
   }
   uint32_t word = 0;
 #pragma unroll
-  for (int i = 0; i < P; ++i) word |= code(v[i], s, b, kMaxQ) << (i * BITS);
+  for (int i = 0; i < P; ++i) word |= clamp_code(r[i], kMaxQ) << (i * BITS);
   packed[t] = word;
 }
 
@@ -154,21 +186,36 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* packed,
 
 unsigned blocks_for(int64_t threads) { return static_cast<unsigned>((threads + 255) / 256); }
 
-template <int BITS, typename WT>
-hipError_t launch_words(const void* weights, int64_t total_words, int wpg, uint32_t* packed, void* scales,
-                        void* biases, bool bf16, hipStream_t stream) {
-  hipLaunchKernelGGL((quantize_words_kernel<BITS, WT>), dim3(blocks_for(total_words)), dim3(256), 0, stream,
-                     static_cast<const uint8_t*>(weights), total_words, wpg, packed, scales, biases, bf16);
+template <int BITS, typename WT, int WPG>
+hipError_t launch_words(const void* weights, int64_t total_words, uint32_t* packed, void* scales, void* biases,
+                        bool bf16, hipStream_t stream) {
+  hipLaunchKernelGGL((quantize_words_kernel<BITS, WT, WPG>), dim3(blocks_for(total_words)), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(weights), total_words, packed, scales, biases, bf16);
   return hipGetLastError();
+}
+
+// wpg: words per group, a power of two <= 64.
+template <int BITS, typename WT>
+hipError_t launch_words_wpg(const void* weights, int64_t total_words, int wpg, uint32_t* packed, void* scales,
+                            void* biases, bool bf16, hipStream_t stream) {
+  switch (wpg) {
+    case 1: return launch_words<BITS, WT, 1>(weights, total_words, packed, scales, biases, bf16, stream);
+    case 2: return launch_words<BITS, WT, 2>(weights, total_words, packed, scales, biases, bf16, stream);
+    case 4: return launch_words<BITS, WT, 4>(weights, total_words, packed, scales, biases, bf16, stream);
+    case 8: return launch_words<BITS, WT, 8>(weights, total_words, packed, scales, biases, bf16, stream);
+    case 16: return launch_words<BITS, WT, 16>(weights, total_words, packed, scales, biases, bf16, stream);
+    case 32: return launch_words<BITS, WT, 32>(weights, total_words, packed, scales, biases, bf16, stream);
+    default: return launch_words<BITS, WT, 64>(weights, total_words, packed, scales, biases, bf16, stream);
+  }
 }
 
 template <typename WT>
 hipError_t launch_words_bits(int bits, const void* weights, int64_t total_words, int wpg, uint32_t* packed,
                              void* scales, void* biases, bool bf16, hipStream_t stream) {
   switch (bits) {
-    case 2: return launch_words<2, WT>(weights, total_words, wpg, packed, scales, biases, bf16, stream);
-    case 4: return launch_words<4, WT>(weights, total_words, wpg, packed, scales, biases, bf16, stream);
-    default: return launch_words<8, WT>(weights, total_words, wpg, packed, scales, biases, bf16, stream);
+    case 2: return launch_words_wpg<2, WT>(weights, total_words, wpg, packed, scales, biases, bf16, stream);
+    case 4: return launch_words_wpg<4, WT>(weights, total_words, wpg, packed, scales, biases, bf16, stream);
+    default: return launch_words_wpg<8, WT>(weights, total_words, wpg, packed, scales, biases, bf16, stream);
   }
 }
 

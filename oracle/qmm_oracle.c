@@ -33,7 +33,10 @@
  *   oracle_quantize              build-defined contract (no reference op exists):
  *                                invariants q in range, group min -> 0, group max -> 2^bits-1,
  *                                |dequant - w| <= scale/2 (+ bf16 parameter rounding),
- *                                constant groups, round-trip of already-quantized rows.
+ *                                constant groups, round-trip of already-quantized rows,
+ *                                exact ties (w-b)/s = k + 1/2 to the even code, and
+ *                                quotients near a tie that follow the division where
+ *                                a reciprocal-multiply would round the other way.
  *   oracle_dequantize            the affine formula of docs/core/quantized-inference.md:59-61
  *                                on hand-built words with known nibbles.
  */

@@ -51,6 +51,50 @@ def tie_group(bits: int, group: int) -> tuple[np.ndarray, np.ndarray]:
     return values, codes
 
 
+def _stored_param(value: np.float32, param_dtype: str) -> np.float32:
+    return O.f32_from_bf16(O.bf16_from_f32(value)).reshape(-1)[0] if param_dtype == "bf16" else value
+
+
+def near_tie_group(bits: int, group: int, param_dtype: str) -> np.ndarray:
+    """One quantization group of f32 values with minimum 0 and maximum
+    (2^bits - 1) * c, for the first c of a fixed list whose stored scale s
+    admits values w within 64 ulps of (k + 1/2) s where rint(w * RN(1/s))
+    differs from rint(RN(w / s)): those values first, then values 1 to 3 ulps
+    either side of (k + 1/2) s, k = 0, 1, ... A quantizer that multiplies by
+    a reciprocal of the scale instead of dividing gets some of the first
+    values wrong."""
+    levels = (1 << bits) - 1
+    f32 = np.float32
+    for c in (0.0237, 0.0313, 0.0411, 0.0191, 0.0667):
+        hi = f32(levels * c)
+        s = _stored_param(f32(hi / f32(levels)), param_dtype)
+        inv = f32(f32(1) / s)
+        ties = (np.arange(levels, dtype=f32) + f32(0.5)) * s
+        down, up, near = ties.copy(), ties.copy(), [ties]
+        for _ in range(64):
+            down = np.nextafter(down, f32(-np.inf), dtype=f32)
+            up = np.nextafter(up, f32(np.inf), dtype=f32)
+            near += [down, up]
+        cand = np.concatenate(near)
+        split = cand[np.rint(cand / s) != np.rint(cand * inv)]
+        if split.size:
+            break
+    values = np.zeros(group, f32)
+    values[min(1, group - 1)] = hi
+    steps = (-3, -2, -1, 1, 2, 3)
+    for i in range(2, group):
+        if i - 2 < split.size:
+            values[i] = split[i - 2]
+            continue
+        k = (i - 2) % levels
+        v = f32(f32(k + 0.5) * s)
+        j = steps[((i - 2) // levels) % len(steps)]
+        for _ in range(abs(j)):
+            v = np.nextafter(v, f32(np.inf if j > 0 else -np.inf), dtype=f32)
+        values[i] = v
+    return values
+
+
 def storage(values, dtype: str) -> np.ndarray:
     """Host storage array for an operand given as f64 values: f32, or bf16 bits."""
     f32 = np.asarray(values, dtype=np.float64).astype(np.float32)

@@ -17,7 +17,8 @@ import affon_amd as A
 from affon_amd import _native
 from oracle import oracle as O
 from tests.helpers import (assert_bf16_product_close, assert_close_rtol_atol, fixture_operands, oracle_columns,
-                           pack_codes, peak_tolerance, reference_f64, storage, tie_group, unpack_bytes_le)
+                           near_tie_group, pack_codes, peak_tolerance, reference_f64, storage, tie_group,
+                           unpack_bytes_le)
 from tests.test_oracle import crossing_word_case, tile_edge_case
 
 pytestmark = pytest.mark.gpu
@@ -580,6 +581,15 @@ def test_quantize_bit_exact(session, bits, group, w_dtype, p_dtype):
     # exact ties k + 1/2 for the stored scale and bias: rounding half to even is observable
     ties, tie_codes = tie_group(bits, group)
     w[5, group:2 * group] = O.bf16_from_f32(ties) if w_dtype == "bf16" else ties
+    # quotients a few ulps from k + 1/2 for a scale that is not a power of two
+    near = near_tie_group(bits, group, p_dtype)
+    w[6, :group] = O.bf16_from_f32(near) if w_dtype == "bf16" else near
+    # NaN as a group's first value, as the first value of a later word of a
+    # group, and inside a word: the group's scale and codes follow the
+    # comparison scan from the group's first value
+    nan = O.bf16_from_f32(np.float32(np.nan)).reshape(-1)[0] if w_dtype == "bf16" else np.float32(np.nan)
+    for c in [0, 2 * group + 1] + ([group + per_word] if group > per_word else []):
+        w[7, c] = nan
     expected = O.quantize(w, bits, group, p_dtype)
     np.testing.assert_array_equal(unpack_bytes_le(expected[0], bits)[5, group:2 * group], tie_codes)
     packed, scales, biases = A.quantize(upload(session, w, w_dtype), bits=bits, group_size=group,

@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import (fixture_operands, pack_codes, reference_f64, storage, tie_group, unpack_bytes_le,
-                           widened)
+from tests.helpers import (fixture_operands, near_tie_group, pack_codes, reference_f64, storage, tie_group,
+                           unpack_bytes_le, widened)
 
 
 def _operands(case):
@@ -310,6 +310,29 @@ def test_quantize_rounds_exact_ties_to_even(bits, group, param_dtype):
         assert widened(scales[1:2, slot:slot + 1])[0, 0] == 0.125 and widened(biases[1:2, slot:slot + 1])[0, 0] == -1.5
     ties = codes[2:2 + max(0, min((1 << bits) - 1, group - 2, 128))]
     assert (ties != np.arange(1, ties.size + 1)).any(), "half-away rounding would give these codes"
+
+
+@pytest.mark.parametrize("bits,group", [(2, 8), (2, 32), (4, 3), (4, 32), (4, 64), (8, 16), (8, 256)])
+@pytest.mark.parametrize("param_dtype", ["f32", "bf16"])
+def test_quantize_near_ties_follow_the_division(bits, group, param_dtype):
+    """The near-tie group of tests.helpers.near_tie_group: the codes are
+    rint((w - b) / s) with the division correctly rounded, and on some values
+    of the group rint((w - b) * RN(1/s)) is another code, so a quantizer that
+    skips the division there fails the GPU test that uses this group."""
+    per_word = 32 // bits
+    cols = int(np.lcm(per_word, group)) * 4
+    values = near_tie_group(bits, group, param_dtype)
+    w = np.zeros((1, cols), np.float32)
+    w[0, :group] = values
+    packed, scales, biases = O.quantize(w, bits, group, param_dtype)
+    s, b = np.float32(widened(scales)[0, 0]), np.float32(widened(biases)[0, 0])
+    assert b == 0.0 and s not in (0.125, 0.25, 0.5)
+    levels = (1 << bits) - 1
+    d = (values - b).astype(np.float32)
+    codes = unpack_bytes_le(packed, bits)[0, :group]
+    np.testing.assert_array_equal(codes, np.clip(np.rint((d / s).astype(np.float32)), 0, levels))
+    by_reciprocal = np.clip(np.rint((d * np.float32(np.float32(1) / s)).astype(np.float32)), 0, levels)
+    assert (by_reciprocal != codes).any()
 
 
 
