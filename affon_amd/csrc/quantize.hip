@@ -184,6 +184,47 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* packed,
   }
 }
 
+// One thread per packed word when a group holds a power of two of whole words
+// (2^wpg_shift): the word's scale and bias are read once, and its P values
+// leave as 16-byte stores (the output is 16-byte aligned). The arithmetic is
+// the general kernel's, s * q + b with two roundings.
+template <int BITS, typename PT, typename OT>
+__global__ __launch_bounds__(256) void dequantize_words_kernel(const uint32_t* packed, const void* scales,
+                                                               const void* biases, int64_t total_words, int wpg_shift,
+                                                               void* out) {
+  constexpr int P = 32 / BITS;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= total_words) return;
+  const uint32_t word = packed[t];
+  const int64_t g = t >> wpg_shift;
+  const float s = load_param<PT>(scales, g);
+  const float b = load_param<PT>(biases, g);
+  uint32_t bits_out[P * OT::bytes / 4];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const float w = s * static_cast<float>((word >> (i * BITS)) & kMask) + b;
+    if constexpr (OT::bytes == 2) {
+      const uint32_t h = f32_to_bf16_bits(w);
+      bits_out[i / 2] = (i % 2 == 0) ? h : (bits_out[i / 2] | (h << 16));
+    } else {
+      bits_out[i] = __float_as_uint(w);
+    }
+  }
+  constexpr int kWords = P * OT::bytes / 4;  // 32-bit words of output per packed word
+  if constexpr (kWords % 4 == 0) {
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(out) + t * (kWords / 4);
+#pragma unroll
+    for (int j = 0; j < kWords / 4; ++j)
+      dst[j] = u32x4_t{bits_out[4 * j], bits_out[4 * j + 1], bits_out[4 * j + 2], bits_out[4 * j + 3]};
+  } else {
+    static_assert(kWords == 2, "8-bit codes to bf16: 8 bytes per word");
+    reinterpret_cast<u32x2_t*>(out)[t] = u32x2_t{bits_out[0], bits_out[1]};
+  }
+}
+
 unsigned blocks_for(int64_t threads) { return static_cast<unsigned>((threads + 255) / 256); }
 
 template <int BITS, typename WT, int WPG>
@@ -239,6 +280,24 @@ hipError_t launch_general(const void* weights, int64_t rows, int64_t columns, in
   return hipGetLastError();
 }
 
+template <int BITS, typename PT, typename OT>
+hipError_t launch_dequantize_words(const uint32_t* packed, const void* scales, const void* biases,
+                                   int64_t total_words, int wpg_shift, void* out, hipStream_t stream) {
+  hipLaunchKernelGGL((dequantize_words_kernel<BITS, PT, OT>), dim3(blocks_for(total_words)), dim3(256), 0, stream,
+                     packed, scales, biases, total_words, wpg_shift, out);
+  return hipGetLastError();
+}
+
+template <typename PT, typename OT>
+hipError_t launch_dequantize_words_bits(int bits, const uint32_t* packed, const void* scales, const void* biases,
+                                        int64_t total_words, int wpg_shift, void* out, hipStream_t stream) {
+  switch (bits) {
+    case 2: return launch_dequantize_words<2, PT, OT>(packed, scales, biases, total_words, wpg_shift, out, stream);
+    case 4: return launch_dequantize_words<4, PT, OT>(packed, scales, biases, total_words, wpg_shift, out, stream);
+    default: return launch_dequantize_words<8, PT, OT>(packed, scales, biases, total_words, wpg_shift, out, stream);
+  }
+}
+
 }  // namespace
 
 hipError_t quantize_launch(const void* weights, int weight_dtype, int64_t rows, int64_t columns, int bits,
@@ -264,7 +323,19 @@ hipError_t quantize_launch(const void* weights, int weight_dtype, int64_t rows, 
 hipError_t dequantize_launch(const uint32_t* packed, const void* scales, const void* biases, int param_dtype,
                              int64_t rows, int64_t columns, int bits, int64_t group, void* out, int out_dtype,
                              hipStream_t stream) {
-  const int64_t total_words = rows * (columns / (32 / bits));
+  const int per_word = 32 / bits;
+  const int64_t total_words = rows * (columns / per_word);
+  const int64_t wpg = group % per_word == 0 ? group / per_word : 0;
+  if (wpg > 0 && (wpg & (wpg - 1)) == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    int shift = 0;
+    while ((int64_t{1} << shift) < wpg) ++shift;
+    const bool pbf = param_dtype == AFFON_ROCM_BF16, obf = out_dtype == AFFON_ROCM_BF16;
+    if (pbf && obf)
+      return launch_dequantize_words_bits<BF16, BF16>(bits, packed, scales, biases, total_words, shift, out, stream);
+    if (pbf) return launch_dequantize_words_bits<BF16, F32>(bits, packed, scales, biases, total_words, shift, out, stream);
+    if (obf) return launch_dequantize_words_bits<F32, BF16>(bits, packed, scales, biases, total_words, shift, out, stream);
+    return launch_dequantize_words_bits<F32, F32>(bits, packed, scales, biases, total_words, shift, out, stream);
+  }
   const dim3 grid(blocks_for(total_words));
   if (param_dtype == AFFON_ROCM_BF16) {
     if (out_dtype == AFFON_ROCM_BF16)

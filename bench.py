@@ -441,6 +441,34 @@ def quantize_stress(session, hip: Hip, steps: int, warmup: int) -> dict:
             "weight_dtype": "f32", "param_dtype": "bf16"}
 
 
+def dequantize_stress(session, hip: Hip, steps: int, warmup: int) -> dict:
+    """Dequantize of the same matrix back to f32: the packed 4-bit codes and
+    bf16 scales and biases of f32 W [28672, 8192] (seed 2, N(0, 0.02), group
+    32, quantized once beforehand) through affon_rocm_dequantize into a
+    preallocated f32 [28672, 8192]. Algorithmic bytes: the codes, both
+    parameter planes and the f32 write (1,086,324,736)."""
+    import affon_amd as A
+    from affon_amd import _native
+    N, K, bits, group = 28672, 8192, 4, 32
+    w = session.randn((N, K), seed=2, std=0.02, dtype="f32")
+    packed, scales, biases = A.quantize(w, bits=bits, group_size=group, param_dtype="bf16")
+    out = session.empty("f32", (N, K))
+    lib = _native.load()
+
+    def launch(i):
+        _native.check(lib.affon_rocm_dequantize(session._handle, packed.data_ptr, scales.data_ptr, biases.data_ptr,
+                                                _native.BF16, N, K, bits, group, out.data_ptr, _native.F32),
+                      "dequantize")
+
+    times = time_graph(hip, session, launch, steps, warmup)
+    t = median(times)
+    nbytes = N * K * bits // 8 + 2 * N * (K // group) * 2 + N * K * 4
+    return {"us_per_step": round(t * 1e3, 3), "us_per_step_replays": [round(v * 1e3, 3) for v in times],
+            "GB/s": round(nbytes / (t * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": nbytes, "shape": [N, K], "bits": bits, "group_size": group,
+            "param_dtype": "bf16", "out_dtype": "f32"}
+
+
 def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
     """Per-launch milliseconds of `steps` launches captured in one HIP graph
     on the session stream, for each of REPLAYS replays (after `warmup`
@@ -718,6 +746,9 @@ def main() -> int:
     if want("quantize_4bit_g32_28672x8192"):
         extras["quantize_4bit_g32_28672x8192"] = quantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
         progress(f"quantize_4bit_g32_28672x8192: {extras['quantize_4bit_g32_28672x8192']['us_per_step']} us per step")
+    if want("dequantize_4bit_g32_28672x8192"):
+        extras["dequantize_4bit_g32_28672x8192"] = dequantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
+        progress(f"dequantize_4bit_g32_28672x8192: {extras['dequantize_4bit_g32_28672x8192']['us_per_step']} us per step")
 
     result = {
         "metric": METRIC,

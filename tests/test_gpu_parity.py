@@ -603,7 +603,8 @@ def test_quantize_bit_exact(session, bits, group, w_dtype, p_dtype):
 
 
 def test_quantize_full_size_stress_bit_exact(session):
-    """f32 [28672, 8192] at 4-bit group 32 with bf16 parameters."""
+    """f32 [28672, 8192] at 4-bit group 32 with bf16 parameters, and its
+    dequantization back to f32 and to bf16."""
     rows, cols = 28672, 8192
     w, _ = O.randn(2, rows * cols, 0.0, 0.02)
     w = w.reshape(rows, cols)
@@ -612,6 +613,11 @@ def test_quantize_full_size_stress_bit_exact(session):
     np.testing.assert_array_equal(packed.storage(), expected[0])
     np.testing.assert_array_equal(scales.storage(), expected[1])
     np.testing.assert_array_equal(biases.storage(), expected[2])
+    del w
+    for out_dtype in ("f32", "bf16"):
+        deq = A.dequantize(packed, scales, biases, bits=4, group_size=32, dtype=out_dtype)
+        np.testing.assert_array_equal(deq.storage(), O.dequantize(*expected, 4, 32, out_dtype))
+        del deq
 
 
 def test_prefill_stress_full_size_sampled(session):
