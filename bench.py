@@ -219,14 +219,15 @@ def _host_cores() -> int:
 
 
 def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, threads: int = 1,
-                 unit: str = "GB/s") -> dict:
+                 unit: str = "GB/s", check_rows: int = 512) -> dict:
     """The reference's scalar CPU kernel as restated in oracle/cpu_baseline.c
     (one specialised loop per bit width and dtype pair, ordered f32, decode
     inside the dot product), timed on this host over a bounded sample of
     about `seconds`: repeated whole passes of the workload, or a prefix of
     output rows when one pass takes longer. With threads > 1 the output rows
     are split over that many threads (the C call releases the interpreter
-    lock). Checks its output against the GPU's and the oracle's."""
+    lock). Checks its output against the GPU's and, on its first
+    `check_rows` output rows, bit for bit against the oracle's."""
     from concurrent.futures import ThreadPoolExecutor
     from oracle import oracle as O
     x, packed, scales, biases = work.host_operands()
@@ -243,7 +244,7 @@ def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, thr
             list(pool.map(call, bounds))
 
     with ThreadPoolExecutor(threads) if threads > 1 else _NullPool() as pool:
-        probe = min(N, 256 * threads)
+        probe = min(N, 256 * threads, max(threads, 4_000_000_000 // (2 * M * K)))  # a few seconds at most
         t0 = time.perf_counter()
         run(probe, pool if threads > 1 else None)
         per_row = (time.perf_counter() - t0) / probe
@@ -257,7 +258,7 @@ def cpu_baseline(work: Workload, gpu_out: np.ndarray, seconds: float = 10.0, thr
     pbytes = 2 if work.p_dtype == "bf16" else 4
     sample_bytes = passes * algorithmic_bytes(M, rows, K, work.bits, work.group, xbytes, pbytes)
     sample_flops = passes * 2 * M * rows * K
-    check = min(rows, 512)
+    check = min(rows, check_rows)
     ref = O.quantized_matmul(x, packed, scales, biases, work.bits, work.group, n_range=(0, check))
     if not np.array_equal(out[:, :check].view(np.uint32), ref[:, :check].view(np.uint32)):
         raise AssertionError("CPU baseline loop differs from the oracle")
@@ -695,9 +696,21 @@ def main() -> int:
             work.release()
         return t
 
+    def with_cpu_baseline(name, work, unit, check_rows=512):
+        """The restated CPU kernel beside a recorded line: one thread, about
+        half the headline's sample time."""
+        if args.cpu_seconds > 0:
+            extras[name]["cpu_baseline"] = cpu_baseline(work, work.out.numpy(), args.cpu_seconds / 2, unit=unit,
+                                                        check_rows=check_rows)
+            progress(f"{name} CPU baseline: {extras[name]['cpu_baseline']['value']} {unit} on 1 thread")
+        work.release()
+
     for M in (1, 2, 4, 8, 16):
         if want(f"decode_8bit_g64_m{M}"):
-            record(f"decode_8bit_g64_m{M}", Workload(session, f"decode_8bit_g64_m{M}", M, 14336, 4096, 8, 64))
+            work = Workload(session, f"decode_8bit_g64_m{M}", M, 14336, 4096, 8, 64)
+            record(f"decode_8bit_g64_m{M}", work, keep=M == 1)
+            if M == 1:
+                with_cpu_baseline(f"decode_8bit_g64_m{M}", work, "GB/s")
     roofline_prefill = None
     for name, N, K in (("prefill_4bit_g64_m512_n14336_k4096", 14336, 4096),
                        ("prefill_4bit_g64_m512_n4096_k14336", 4096, 14336)):
@@ -724,8 +737,13 @@ def main() -> int:
     for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192", 28672, 8192),
                        ("prefill_4bit_g32_m2048_n8192_k28672", 8192, 28672)):
         if want(name):
-            record(name, Workload(session, name, 2048, N, K, 4, 32, policy="approximate"), bound="mfma")
+            work = Workload(session, name, 2048, N, K, 4, 32, policy="approximate")
+            record(name, work, bound="mfma", keep=True)
             extras[name]["numerical_policy"] = "approximate"
+            if N == 28672:  # the CPU kernel on a prefix of the output columns (every activation row)
+                with_cpu_baseline(name, work, "TFLOP/s", check_rows=16)
+            else:
+                work.release()
     # The same stress shapes under the default policy (the group-32 reassociated GEMM).
     for name, N, K in (("prefill_4bit_g32_m2048_n28672_k8192_backend_equivalent", 28672, 8192),
                        ("prefill_4bit_g32_m2048_n8192_k28672_backend_equivalent", 8192, 28672)):
@@ -741,8 +759,9 @@ def main() -> int:
                 extras[name] = layer_sequence(session, hip, M, args.steps // 10 or 1, args.warmup, fused=fused)
                 progress(f"{name}: {extras[name]['us_per_layer']} us per layer")
     if want("decode_4bit_g64_f32_4096"):
-        record("decode_4bit_g64_f32_4096", Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64,
-                                                    x_dtype="f32", p_dtype="f32"))
+        work = Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64, x_dtype="f32", p_dtype="f32")
+        record("decode_4bit_g64_f32_4096", work, keep=True)
+        with_cpu_baseline("decode_4bit_g64_f32_4096", work, "GB/s")
     if want("quantize_4bit_g32_28672x8192"):
         extras["quantize_4bit_g32_28672x8192"] = quantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
         progress(f"quantize_4bit_g32_28672x8192: {extras['quantize_4bit_g32_28672x8192']['us_per_step']} us per step")
