@@ -275,8 +275,9 @@ int compute_core_run_quantized_matmul_f32(const float* activation, size_t activa
  * (max - min) / (2^bits - 1), bias = min (signed zeros canonicalised to +0),
  * both stored as param_dtype (bf16: round to nearest even), q =
  * clamp(rint((w - bias) / scale), 0, 2^bits - 1) from the stored scale and
- * bias with IEEE f32 division, q = 0 when the stored scale is 0.
- * Inputs must be finite. */
+ * bias with IEEE f32 division, q = 0 when the stored scale is 0. min and
+ * max are a comparison scan from each group's first value: a NaN there gives
+ * a NaN scale and bias and codes 0; a later NaN is skipped and takes code 0. */
 int affon_rocm_quantize(affon_rocm_session* session, const void* weights, int32_t weight_dtype,
                         int64_t rows, int64_t columns, uint32_t bits, uint32_t group_size,
                         uint32_t* packed, void* scales, void* biases, int32_t param_dtype);
