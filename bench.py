@@ -281,6 +281,37 @@ class _NullPool:
         return False
 
 
+def host_entry(work: Workload, calls: int = 50, warmup: int = 5) -> dict:
+    """The drop-in host entry compute_core_run_quantized_matmul_f32 (the
+    reference's Cyna C ABI, f32 operands in host memory) over the workload's
+    own operands: each call allocates the device buffers, copies every
+    operand in from pageable host memory, launches, copies the output back and
+    frees. Wall-clock per synchronous call from this Python caller; the
+    median over `calls`. The PCIe-inclusive rate, never the headline."""
+    from affon_amd import _native
+    x, packed, scales, biases = work.host_operands()
+    out = np.empty((work.M, work.N), dtype=np.float32)
+    lib = _native.load()
+    args = (x.ctypes.data, x.size, packed.ctypes.data, packed.size, scales.ctypes.data, scales.size,
+            biases.ctypes.data, biases.size, out.ctypes.data, out.size, work.M, work.K, work.N, work.bits, work.group)
+    times = []
+    for i in range(warmup + calls):
+        t0 = time.perf_counter()
+        status = lib.compute_core_run_quantized_matmul_f32(*args)
+        if status != 0:
+            raise RuntimeError(f"compute_core_run_quantized_matmul_f32 returned {status}: {_native.last_error()}")
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    t = median(times)
+    gpu = work.out.numpy()
+    if not np.array_equal(out.view(np.uint32), gpu.view(np.uint32)):
+        raise AssertionError("host entry output differs from the device launch")
+    return {"us_per_call": round(t * 1e6, 1), "GB/s": round(work.bytes / t / 1e9, 2), "calls": calls,
+            "includes": "device allocation of the five buffers, host-to-device copies of every operand from pageable "
+                        "host memory, the launch, the device-to-host copy of the output and the frees; synchronous, "
+                        "Python caller"}
+
+
 def end_to_end(work: Workload, calls: int = 200) -> dict:
     """One call as the reference's benchmark times it: launch, then read the
     output back to the host (the host read synchronises), per call, from
@@ -761,6 +792,9 @@ def main() -> int:
     if want("decode_4bit_g64_f32_4096"):
         work = Workload(session, "decode_4bit_g64_f32_4096", 1, 4096, 4096, 4, 64, x_dtype="f32", p_dtype="f32")
         record("decode_4bit_g64_f32_4096", work, keep=True)
+        extras["decode_4bit_g64_f32_4096"]["host_entry"] = host_entry(work)
+        progress(f"decode_4bit_g64_f32_4096 through the host entry: "
+                 f"{extras['decode_4bit_g64_f32_4096']['host_entry']['us_per_call']} us per call")
         with_cpu_baseline("decode_4bit_g64_f32_4096", work, "GB/s")
     if want("quantize_4bit_g32_28672x8192"):
         extras["quantize_4bit_g32_28672x8192"] = quantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
