@@ -501,6 +501,29 @@ def dequantize_stress(session, hip: Hip, steps: int, warmup: int) -> dict:
             "param_dtype": "bf16", "out_dtype": "f32"}
 
 
+def reference_workload(session, hip: Hip, steps: int, warmup: int) -> dict:
+    """The workload of the reference's own published timings
+    (docs/core/quantized-inference.md:315-320, Apple M4): 8-bit codes,
+    N = 2048, K = 1024, group 64, f32 activations, bf16 scales and biases,
+    f32 output, M = 1, 8, 32 and 128, seeded as the other lines. Per M: the
+    graph-replay period of the launch on resident operands, and one call with
+    full readback (launch, then the synchronous copy of the output to the
+    host), the kind of figure those timings are (0.400 / 1.033 / 2.500 /
+    8.667 ms for Affon's Metal path there)."""
+    result = {}
+    for M in (1, 8, 32, 128):
+        work = Workload(session, f"reference_8bit_g64_n2048_k1024_m{M}", M, 2048, 1024, 8, 64, x_dtype="f32",
+                        p_dtype="bf16")
+        t = work.time(hip, steps, warmup, True)
+        e2e = end_to_end(work)
+        result[f"m{M}"] = {"implementation": work.implementation, "us_per_step": round(t * 1e3, 3),
+                           "us_per_step_replays": [round(v * 1e3, 3) for v in work.replay_ms],
+                           "GB/s": round(work.bytes / (t * 1e-3) / 1e9, 1),
+                           "full_readback_us_per_call": e2e["us_per_call"]}
+        work.release()
+    return result
+
+
 def time_graph(hip: Hip, session, launch, steps: int, warmup: int) -> list:
     """Per-launch milliseconds of `steps` launches captured in one HIP graph
     on the session stream, for each of REPLAYS replays (after `warmup`
@@ -799,6 +822,11 @@ def main() -> int:
     if want("quantize_4bit_g32_28672x8192"):
         extras["quantize_4bit_g32_28672x8192"] = quantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
         progress(f"quantize_4bit_g32_28672x8192: {extras['quantize_4bit_g32_28672x8192']['us_per_step']} us per step")
+    if want("reference_8bit_g64_n2048_k1024"):
+        extras["reference_8bit_g64_n2048_k1024"] = reference_workload(session, hip, args.steps, args.warmup)
+        progress("reference_8bit_g64_n2048_k1024: " + ", ".join(
+            f"{m}: {v['us_per_step']} us, {v['full_readback_us_per_call']} us with readback"
+            for m, v in extras["reference_8bit_g64_n2048_k1024"].items()))
     if want("dequantize_4bit_g32_28672x8192"):
         extras["dequantize_4bit_g32_28672x8192"] = dequantize_stress(session, hip, args.steps // 10 or 1, args.warmup)
         progress(f"dequantize_4bit_g32_28672x8192: {extras['dequantize_4bit_g32_28672x8192']['us_per_step']} us per step")
