@@ -184,14 +184,16 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const uint32_t* packed,
   }
 }
 
-// One thread per packed word when a group holds a power of two of whole words
-// (2^wpg_shift): the word's scale and bias are read once, and its P values
-// leave as 16-byte stores (the output is 16-byte aligned). The arithmetic is
-// the general kernel's, s * q + b with two roundings.
+// One thread per packed word when a group holds whole words (wpg of them:
+// the group index is t >> wpg_shift for a power of two, else a 32-bit
+// division, the word count then below 2^32): the word's scale and bias are
+// read once, and its P values leave as 16-byte stores (the output is 16-byte
+// aligned). The arithmetic is the general kernel's, s * q + b with two
+// roundings.
 template <int BITS, typename PT, typename OT>
 __global__ __launch_bounds__(256) void dequantize_words_kernel(const uint32_t* packed, const void* scales,
                                                                const void* biases, int64_t total_words, int wpg_shift,
-                                                               void* out) {
+                                                               uint32_t wpg, void* out) {
   constexpr int P = 32 / BITS;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(256) void dequantize_words_kernel(const uint32_t* p
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= total_words) return;
   const uint32_t word = packed[t];
-  const int64_t g = t >> wpg_shift;
+  const int64_t g = wpg_shift >= 0 ? t >> wpg_shift : static_cast<int64_t>(static_cast<uint32_t>(t) / wpg);
   const float s = load_param<PT>(scales, g);
   const float b = load_param<PT>(biases, g);
   uint32_t bits_out[P * OT::bytes / 4];
@@ -282,19 +284,21 @@ hipError_t launch_general(const void* weights, int64_t rows, int64_t columns, in
 
 template <int BITS, typename PT, typename OT>
 hipError_t launch_dequantize_words(const uint32_t* packed, const void* scales, const void* biases,
-                                   int64_t total_words, int wpg_shift, void* out, hipStream_t stream) {
+                                   int64_t total_words, int wpg_shift, uint32_t wpg, void* out, hipStream_t stream) {
   hipLaunchKernelGGL((dequantize_words_kernel<BITS, PT, OT>), dim3(blocks_for(total_words)), dim3(256), 0, stream,
-                     packed, scales, biases, total_words, wpg_shift, out);
+                     packed, scales, biases, total_words, wpg_shift, wpg, out);
   return hipGetLastError();
 }
 
 template <typename PT, typename OT>
 hipError_t launch_dequantize_words_bits(int bits, const uint32_t* packed, const void* scales, const void* biases,
-                                        int64_t total_words, int wpg_shift, void* out, hipStream_t stream) {
+                                        int64_t total_words, int wpg_shift, uint32_t wpg, void* out,
+                                        hipStream_t stream) {
   switch (bits) {
-    case 2: return launch_dequantize_words<2, PT, OT>(packed, scales, biases, total_words, wpg_shift, out, stream);
-    case 4: return launch_dequantize_words<4, PT, OT>(packed, scales, biases, total_words, wpg_shift, out, stream);
-    default: return launch_dequantize_words<8, PT, OT>(packed, scales, biases, total_words, wpg_shift, out, stream);
+    case 2: return launch_dequantize_words<2, PT, OT>(packed, scales, biases, total_words, wpg_shift, wpg, out, stream);
+    case 4: return launch_dequantize_words<4, PT, OT>(packed, scales, biases, total_words, wpg_shift, wpg, out, stream);
+    default:
+      return launch_dequantize_words<8, PT, OT>(packed, scales, biases, total_words, wpg_shift, wpg, out, stream);
   }
 }
 
@@ -326,15 +330,22 @@ hipError_t dequantize_launch(const uint32_t* packed, const void* scales, const v
   const int per_word = 32 / bits;
   const int64_t total_words = rows * (columns / per_word);
   const int64_t wpg = group % per_word == 0 ? group / per_word : 0;
-  if (wpg > 0 && (wpg & (wpg - 1)) == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0) {
-    int shift = 0;
-    while ((int64_t{1} << shift) < wpg) ++shift;
+  const bool pow2 = wpg > 0 && (wpg & (wpg - 1)) == 0;
+  if (wpg > 0 && (pow2 || (total_words <= 0xffffffffll && wpg <= 0xffffffffll)) &&
+      reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    int shift = -1;
+    if (pow2)
+      for (shift = 0; (int64_t{1} << shift) < wpg;) ++shift;
+    const uint32_t w32 = static_cast<uint32_t>(wpg);
     const bool pbf = param_dtype == AFFON_ROCM_BF16, obf = out_dtype == AFFON_ROCM_BF16;
     if (pbf && obf)
-      return launch_dequantize_words_bits<BF16, BF16>(bits, packed, scales, biases, total_words, shift, out, stream);
-    if (pbf) return launch_dequantize_words_bits<BF16, F32>(bits, packed, scales, biases, total_words, shift, out, stream);
-    if (obf) return launch_dequantize_words_bits<F32, BF16>(bits, packed, scales, biases, total_words, shift, out, stream);
-    return launch_dequantize_words_bits<F32, F32>(bits, packed, scales, biases, total_words, shift, out, stream);
+      return launch_dequantize_words_bits<BF16, BF16>(bits, packed, scales, biases, total_words, shift, w32, out,
+                                                      stream);
+    if (pbf)
+      return launch_dequantize_words_bits<BF16, F32>(bits, packed, scales, biases, total_words, shift, w32, out, stream);
+    if (obf)
+      return launch_dequantize_words_bits<F32, BF16>(bits, packed, scales, biases, total_words, shift, w32, out, stream);
+    return launch_dequantize_words_bits<F32, F32>(bits, packed, scales, biases, total_words, shift, w32, out, stream);
   }
   const dim3 grid(blocks_for(total_words));
   if (param_dtype == AFFON_ROCM_BF16) {
